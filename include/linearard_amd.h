@@ -1,0 +1,109 @@
+/*
+ * linearard_amd.h -- C ABI of the MI355X (gfx950) attention-relation KL library.
+ *
+ * This is the drop-in boundary for LinearARD's linear-memory attention KL
+ * (reference: kernels/attention_KL/).  Each entry point replaces one
+ * reference interface; the citation is on the declaration.  The library is
+ * `linearard_amd/liblinearard_amd.so`.
+ *
+ * Conventions
+ *   - Every tensor argument is a device pointer the caller owns.  The
+ *     library never allocates or frees device memory; scratch space is
+ *     passed in by the caller, sized by the matching *_workspace_bytes().
+ *   - q/k tensors are [B, H, T, D] with element strides; stride[3] must be 1,
+ *     the data pointer 16-byte aligned and strides[0..2] multiples of 8
+ *     (every contiguous tensor with D in {8,16,32,64,128,256} qualifies).
+ *   - Outputs (lse, dq, dk, dx) are contiguous float32 of the stated shape.
+ *   - GQA: kv head of query head h is h / (Hq / Hkv)   (kernel_A.py:77).
+ *   - All work is enqueued on `stream` (a hipStream_t) and is asynchronous;
+ *     no entry point synchronises the host.  Calls are reentrant; the only
+ *     library state is the thread-local error string.
+ *   - Return value: LARD_OK (0) or a negative LARD_ERR_* code; the message
+ *     is available from lard_last_error() on the calling thread.
+ */
+#ifndef LINEARARD_AMD_H
+#define LINEARARD_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LARD_OK 0
+#define LARD_ERR_INVALID_ARGUMENT (-1)
+#define LARD_ERR_UNSUPPORTED (-2)
+#define LARD_ERR_HIP (-3)
+
+/* element type of q / k (kernel_A.py:195-196 accepts fp16 and bf16 only) */
+#define LARD_DTYPE_F16 0
+#define LARD_DTYPE_BF16 1
+
+/* attention-mask element type, [B, T], nonzero = valid token (kernel_A.py:218) */
+#define LARD_MASK_NONE 0
+#define LARD_MASK_U8 1 /* torch.bool or torch.uint8 */
+#define LARD_MASK_I32 2
+#define LARD_MASK_I64 3
+
+typedef struct lard_tensor4 {
+  const void* data;  /* device pointer */
+  int64_t size[4];   /* B, H, T, D */
+  int64_t stride[4]; /* element strides, stride[3] == 1 */
+  int32_t dtype;     /* LARD_DTYPE_* */
+} lard_tensor4;
+
+typedef struct lard_mask {
+  const void* data;  /* device pointer, ignored when kind == LARD_MASK_NONE */
+  int32_t kind;      /* LARD_MASK_* */
+  int64_t size[2];   /* B, T */
+  int64_t stride[2]; /* element strides, stride[1] == 1 */
+} lard_mask;
+
+/* Library version string, e.g. "linearard_amd 0.1.0 gfx950". */
+const char* lard_version(void);
+
+/* Message of the last failed call on this thread ("" after a success). */
+const char* lard_last_error(void);
+
+/*
+ * Stage A -- replaces lse_stats_triton(q, k, attn_mask, causal, sm_scale)
+ * (kernel_A.py:190-265).  Writes lse[B, Hq, T] (float32, contiguous):
+ * log sum_j exp(sm_scale q_i.k_j) over the valid set, 0 for masked rows.
+ * `mask` may be NULL (no padding).
+ */
+int lard_lse_stats(const lard_tensor4* q, const lard_tensor4* k, const lard_mask* mask,
+                   int causal, float sm_scale, float* lse_out, void* stream);
+
+/* Workspace needed by lard_kl_forward for B x Hq x T rows (bytes). */
+size_t lard_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len);
+
+/*
+ * Stage B -- replaces kl_forward_triton(qs, ks, lse_s, qt, kt, lse_t,
+ * attn_mask, causal, sm_scale_s, sm_scale_t)  (kernel_B.py:249-391).
+ * Writes the 0-d float32 SUM over rows of sum_j p_t (log p_t - log p_s) to
+ * loss_out[0].  lse_s / lse_t are contiguous float32 [B, Hq, T].  The sum is
+ * deterministic (fixed-order reduction; the reference uses atomics).
+ */
+int lard_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s,
+                    const lard_tensor4* qt, const lard_tensor4* kt, const float* lse_t,
+                    const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
+                    float* loss_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Stage C -- replaces kl_backward_triton(...)  (kernel_C.py:293-449).
+ * Writes dq[B, Hq, T, Ds] and dk[B, Hkv_s, T, Ds] (float32, contiguous,
+ * every element written): D = p_s - p_t cast to the student dtype,
+ * dq = sm_scale_s D K_s, dk = sm_scale_s sum_{h in group} D^T Q_s.
+ * dk is accumulated by one owner per key tile (no atomics).
+ */
+int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s,
+                     const lard_tensor4* qt, const lard_tensor4* kt, const float* lse_t,
+                     const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
+                     float* dq_out, float* dk_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LINEARARD_AMD_H */

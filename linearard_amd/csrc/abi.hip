@@ -1,0 +1,233 @@
+// C ABI entry points: argument validation, descriptor packing, dispatch.
+//
+// Validation restates the preconditions of the reference wrappers
+// (kernel_A.py:192-220, kernel_B.py:262-322, kernel_C.py:307-368) as error
+// returns, plus the alignment rules of the 16-byte vector loads.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/linearard_amd.h"
+#include "stage_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return LARD_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(LARD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool supported_dim(int64_t d) {
+  return d == 8 || d == 16 || d == 32 || d == 64 || d == 128 || d == 256;  // kernel_A.py:18
+}
+
+int padded_dim(int64_t d) { return d < 16 ? 16 : (int)d; }
+
+int check_tensor(const lard_tensor4* t, const char* name) {
+  if (t == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
+  if (t->data == nullptr && t->size[0] * t->size[1] * t->size[2] * t->size[3] != 0)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "%s data pointer is NULL", name);
+  for (int i = 0; i < 4; ++i)
+    if (t->size[i] < 0) return fail(LARD_ERR_INVALID_ARGUMENT, "%s has a negative size", name);
+  if (t->dtype != LARD_DTYPE_F16 && t->dtype != LARD_DTYPE_BF16)
+    return fail(LARD_ERR_UNSUPPORTED, "%s dtype supports only fp16/bf16", name);
+  if (t->stride[3] != 1) return fail(LARD_ERR_INVALID_ARGUMENT, "%s last-dim stride must be 1", name);
+  for (int i = 0; i < 3; ++i)
+    if (t->stride[i] % 8 != 0)
+      return fail(LARD_ERR_UNSUPPORTED, "%s strides must be multiples of 8 elements", name);
+  if (reinterpret_cast<uintptr_t>(t->data) % 16 != 0)
+    return fail(LARD_ERR_UNSUPPORTED, "%s data pointer must be 16-byte aligned", name);
+  if (t->size[2] > (int64_t)1 << 30) return fail(LARD_ERR_UNSUPPORTED, "%s sequence length too large", name);
+  return LARD_OK;
+}
+
+// Checks a (q, k) relation pair (kernel_A.py:192-208).
+int check_pair(const lard_tensor4* q, const lard_tensor4* k, const char* qn, const char* kn) {
+  int rc;
+  if ((rc = check_tensor(q, qn)) != LARD_OK) return rc;
+  if ((rc = check_tensor(k, kn)) != LARD_OK) return rc;
+  if (q->dtype != k->dtype) return fail(LARD_ERR_INVALID_ARGUMENT, "%s/%s dtype must match", qn, kn);
+  if (q->size[0] != k->size[0]) return fail(LARD_ERR_INVALID_ARGUMENT, "%s/%s B must match", qn, kn);
+  if (q->size[2] != k->size[2]) return fail(LARD_ERR_INVALID_ARGUMENT, "%s/%s T must match", qn, kn);
+  if (q->size[3] != k->size[3]) return fail(LARD_ERR_INVALID_ARGUMENT, "%s/%s D must match", qn, kn);
+  if (!supported_dim(q->size[3])) return fail(LARD_ERR_UNSUPPORTED, "D is not in the supported set");
+  if (k->size[1] <= 0 && q->size[1] > 0) return fail(LARD_ERR_INVALID_ARGUMENT, "%s has no heads", kn);
+  if (k->size[1] > 0 && q->size[1] % k->size[1] != 0)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "Hq must be divisible by Hkv");
+  return LARD_OK;
+}
+
+int check_mask(const lard_mask* m, int64_t B, int64_t T) {
+  if (m == nullptr || m->kind == LARD_MASK_NONE) return LARD_OK;
+  if (m->kind != LARD_MASK_U8 && m->kind != LARD_MASK_I32 && m->kind != LARD_MASK_I64)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "attn_mask dtype is invalid");
+  if (m->size[0] != B || m->size[1] != T) return fail(LARD_ERR_INVALID_ARGUMENT, "attn_mask shape must be [B,T]");
+  if (m->stride[1] != 1 && T > 1) return fail(LARD_ERR_INVALID_ARGUMENT, "attn_mask last-dim stride must be 1");
+  if (m->data == nullptr && B * T != 0) return fail(LARD_ERR_INVALID_ARGUMENT, "attn_mask data pointer is NULL");
+  return LARD_OK;
+}
+
+void fill_side(lard::SideArgs& s, const lard_tensor4* q, const lard_tensor4* k, int64_t Hq, float scale) {
+  s.q = static_cast<const lard::u16*>(q->data);
+  s.k = static_cast<const lard::u16*>(k->data);
+  s.q_sb = q->stride[0];
+  s.q_sh = q->stride[1];
+  s.q_st = q->stride[2];
+  s.k_sb = k->stride[0];
+  s.k_sh = k->stride[1];
+  s.k_st = k->stride[2];
+  s.hkv = (int)k->size[1];
+  s.group = (int)(Hq / k->size[1]);
+  s.dim = (int)q->size[3];
+  s.bf16 = q->dtype == LARD_DTYPE_BF16;
+  s.scale = scale;
+  s.scale2 = scale * lard::kLog2e;
+}
+
+void fill_common(lard::RelArgs& a, int64_t B, int64_t Hq, int64_t T, const lard_mask* m, int causal) {
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.T = (int)T;
+  a.causal = causal ? 1 : 0;
+  if (m != nullptr && m->kind != LARD_MASK_NONE) {
+    a.mask = m->data;
+    a.mask_kind = m->kind;
+    a.mask_sb = m->stride[0];
+  } else {
+    a.mask = nullptr;
+    a.mask_kind = 0;
+    a.mask_sb = 0;
+  }
+}
+
+int check_grid(int64_t rows) {
+  if (rows > 65536) return fail(LARD_ERR_UNSUPPORTED, "B * heads must be <= 65536");
+  return LARD_OK;
+}
+
+int check_scale(float s, const char* name) {
+  if (!std::isfinite(s)) return fail(LARD_ERR_INVALID_ARGUMENT, "%s must be a finite scalar", name);
+  return LARD_OK;
+}
+
+// Stage B / C share their argument checks (kernel_B.py:262-322).
+int check_two_sided(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
+                    const lard_tensor4* kt, const float* lse_t, const lard_mask* mask, float ss, float st) {
+  int rc;
+  if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
+  if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
+  if (qs->size[0] != qt->size[0] || qs->size[1] != qt->size[1] || qs->size[2] != qt->size[2])
+    return fail(LARD_ERR_INVALID_ARGUMENT, "student/teacher B/Hq/T must align");
+  const int64_t n = qs->size[0] * qs->size[1] * qs->size[2];
+  if (n > 0 && (lse_s == nullptr || lse_t == nullptr)) return fail(LARD_ERR_INVALID_ARGUMENT, "lse must not be NULL");
+  if ((rc = check_mask(mask, qs->size[0], qs->size[2])) != LARD_OK) return rc;
+  if ((rc = check_scale(ss, "sm_scale_s")) != LARD_OK) return rc;
+  if ((rc = check_scale(st, "sm_scale_t")) != LARD_OK) return rc;
+  return check_grid(qs->size[0] * (qs->size[1] > ks->size[1] ? qs->size[1] : ks->size[1]));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lard_version(void) { return "linearard_amd 0.1.0 gfx950"; }
+
+const char* lard_last_error(void) { return g_last_error.c_str(); }
+
+int lard_lse_stats(const lard_tensor4* q, const lard_tensor4* k, const lard_mask* mask, int causal, float sm_scale,
+                   float* lse_out, void* stream) {
+  int rc;
+  if ((rc = check_pair(q, k, "q", "k")) != LARD_OK) return rc;
+  if ((rc = check_mask(mask, q->size[0], q->size[2])) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale, "sm_scale")) != LARD_OK) return rc;
+  const int64_t B = q->size[0], Hq = q->size[1], T = q->size[2];
+  if (B * Hq * T == 0) return ok();
+  if (lse_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "lse_out must not be NULL");
+  if ((rc = check_grid(B * Hq)) != LARD_OK) return rc;
+  lard::RelArgs a{};
+  fill_side(a.s, q, k, Hq, sm_scale);
+  a.t = a.s;
+  fill_common(a, B, Hq, T, mask, causal);
+  a.lse_out = lse_out;
+  return hip_status(lard::launch_row_lse(a, padded_dim(q->size[3]), static_cast<hipStream_t>(stream)),
+                    "lse_stats launch");
+}
+
+size_t lard_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
+  if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  return (size_t)(batch * heads * seq_len) * sizeof(float);
+}
+
+int lard_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
+                    const lard_tensor4* kt, const float* lse_t, const lard_mask* mask, int causal, float sm_scale_s,
+                    float sm_scale_t, float* loss_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_two_sided(qs, ks, lse_s, qt, kt, lse_t, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  if (loss_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "loss_out must not be NULL");
+  const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = B * Hq * T;
+  if (n > 0) {
+    if (workspace == nullptr || workspace_bytes < lard_kl_forward_workspace_bytes(B, Hq, T))
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes",
+                  lard_kl_forward_workspace_bytes(B, Hq, T));
+    lard::RelArgs a{};
+    fill_side(a.s, qs, ks, Hq, sm_scale_s);
+    fill_side(a.t, qt, kt, Hq, sm_scale_t);
+    fill_common(a, B, Hq, T, mask, causal);
+    a.lse_s_in = lse_s;
+    a.lse_t_in = lse_t;
+    a.row_out = static_cast<float*>(workspace);
+    if ((rc = hip_status(lard::launch_row_kl(a, padded_dim(qs->size[3]), padded_dim(qt->size[3]), st),
+                         "kl_forward launch")) != LARD_OK)
+      return rc;
+  }
+  return hip_status(lard::launch_reduce_sum(static_cast<const float*>(workspace), n, loss_out, st),
+                    "kl_forward reduce launch");
+}
+
+int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
+                     const lard_tensor4* kt, const float* lse_t, const lard_mask* mask, int causal, float sm_scale_s,
+                     float sm_scale_t, float* dq_out, float* dk_out, void* stream) {
+  int rc;
+  if ((rc = check_two_sided(qs, ks, lse_s, qt, kt, lse_t, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
+  if (B * Hq * T == 0) return ok();
+  if (dq_out == nullptr || dk_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "dq_out/dk_out must not be NULL");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  lard::RelArgs a{};
+  fill_side(a.s, qs, ks, Hq, sm_scale_s);
+  fill_side(a.t, qt, kt, Hq, sm_scale_t);
+  fill_common(a, B, Hq, T, mask, causal);
+  a.lse_s_in = lse_s;
+  a.lse_t_in = lse_t;
+  a.dq_out = dq_out;
+  a.dk_out = dk_out;
+  const int dps = padded_dim(qs->size[3]), dpt = padded_dim(qt->size[3]);
+  if ((rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "kl_backward dq launch")) != LARD_OK) return rc;
+  return hip_status(lard::launch_col_dk(a, dps, dpt, st), "kl_backward dk launch");
+}
+
+}  // extern "C"

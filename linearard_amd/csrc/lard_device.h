@@ -1,0 +1,154 @@
+// Device-side building blocks shared by every attention-relation KL kernel.
+//
+// Conventions used throughout (gfx950 / CDNA4, wave64):
+//   * One MFMA tile is v_mfma_f32_32x32x16_{bf16,f16}: C[32x32] += A[32x16] B[16x32].
+//     Lane l supplies A[m = l%32][k-slot 8*(l/32)+e] and B[k-slot 8*(l/32)+e][n = l%32]
+//     (e = 0..7).  The k-slot order inside a lane is free as long as A and B use
+//     the same one; the kernels exploit that to feed register-resident
+//     probability tiles straight into the second GEMM.
+//   * The 16 accumulator registers of lane l hold C[m][n] with
+//     n = l%32 and m = 8*(r/4) + 4*(l/32) + r%4.
+//   * Stage kernels keep logits, maxima and LSE in natural-log units like
+//     the reference (scores = dot * sm_scale, kernel_A.py:135), so that
+//     S - lse is exactly 0 for a single-entry row; exp(x) is evaluated as
+//     v_exp_f32(x * log2(e)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lard {
+
+typedef unsigned short u16;
+typedef u16 u16x8 __attribute__((ext_vector_type(8)));
+typedef u16 u16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Kernel modes of the row-owner template.
+enum RowMode : int {
+  MODE_LSE = 0,  // stage A: one relation's row LSE           (kernel_A.py:42-159)
+  MODE_KL = 1,   // stage B: per-row KL given both LSE vectors (kernel_B.py:57-218)
+  MODE_DQ = 2,   // stage C row side: dq = a_s D K_s           (kernel_C.py:224-239)
+};
+
+// One relation q.k^T of the problem (student or teacher).
+struct SideArgs {
+  const u16* q;       // [B, Hq, T, D] elements (bf16 or f16 bits)
+  const u16* k;       // [B, Hkv, T, D]
+  int64_t q_sb, q_sh, q_st;  // element strides (D stride is 1)
+  int64_t k_sb, k_sh, k_st;
+  int hkv;            // Hkv
+  int group;          // Hq / Hkv  (kv head = h / group, kernel_A.py:77)
+  int dim;            // D (<= the kernel's padded D)
+  int bf16;           // 1: bfloat16, 0: float16
+  float scale;        // softmax scale (natural)
+  float scale2;       // scale * log2(e)
+};
+
+struct RelArgs {
+  SideArgs s, t;      // student, teacher
+  int B, Hq, T;
+  int causal;
+  const void* mask;   // [B, T] or null
+  int mask_kind;      // 0 none, 1 one byte (bool/u8), 2 int32, 3 int64
+  int64_t mask_sb;    // batch stride of the mask (T stride is 1)
+  const float* lse_s_in;  // [B, Hq, T] contiguous (modes KL, DQ, and the dk kernel)
+  const float* lse_t_in;
+  float* lse_out;     // [B, Hq, T] (mode LSE)
+  float* row_out;     // [B, Hq, T] per-row KL (mode KL)
+  float* dq_out;      // [B, Hq, T, Ds] fp32 (mode DQ)
+  float* dk_out;      // [B, Hkv_s, T, Ds] fp32 (dk kernel)
+};
+
+__device__ __forceinline__ bool mask_at(const void* m, int kind, int64_t idx) {
+  if (kind == 1) return static_cast<const unsigned char*>(m)[idx] != 0;
+  if (kind == 2) return static_cast<const int32_t*>(m)[idx] != 0;
+  if (kind == 3) return static_cast<const int64_t*>(m)[idx] != 0;
+  return true;
+}
+
+template <bool BF>
+__device__ __forceinline__ f32x16 mfma32(u16x8 a, u16x8 b, f32x16 c) {
+  if constexpr (BF) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Round-to-nearest-even conversion of one float to the 16-bit input type.
+__device__ __forceinline__ u16 to_bits(float x, bool bf) {
+  return bf ? __builtin_bit_cast(u16, static_cast<__bf16>(x))
+            : __builtin_bit_cast(u16, static_cast<_Float16>(x));
+}
+
+// Rounded product that the compiler may not fuse into a following add:
+// the reference forms scores = dot * sm_scale as a rounded fp32 value before
+// subtracting the LSE (kernel_B.py:190, :206), which makes S - lse exactly 0
+// for single-entry rows.  hipcc's default -ffp-contract=fast-honor-pragmas
+// honors this pragma.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// Copy rows [row0, row0+NROWS) x [0, DP) of a [T, D]-strided 16-bit matrix
+// into LDS with row stride LDS_STRIDE (elements).  Rows >= T and columns
+// >= dim are written as zeros, so the MFMA sees exact zero padding.
+template <int NROWS, int DP, int LDS_STRIDE, int NTHREADS>
+__device__ __forceinline__ void stage_rows(u16* lds, const u16* g, int64_t row_stride, int row0,
+                                           int T, int dim, int tid) {
+  constexpr int CPR = DP / 8;  // 16-byte chunks per row
+#pragma unroll
+  for (int c = tid; c < NROWS * CPR; c += NTHREADS) {
+    const int r = c / CPR;
+    const int dc = (c % CPR) * 8;
+    const int row = row0 + r;
+    u16x8 v = (u16x8)(0);
+    if (row < T && dc < dim) v = *reinterpret_cast<const u16x8*>(g + (int64_t)row * row_stride + dc);
+    *reinterpret_cast<u16x8*>(lds + r * LDS_STRIDE + dc) = v;
+  }
+}
+
+// Same source tile, stored transposed: lds[d * LDS_STRIDE + r].
+template <int NROWS, int DP, int LDS_STRIDE, int NTHREADS>
+__device__ __forceinline__ void stage_rows_transposed(u16* lds, const u16* g, int64_t row_stride,
+                                                      int row0, int T, int dim, int tid) {
+  constexpr int CPR = DP / 8;
+#pragma unroll
+  for (int c = tid; c < NROWS * CPR; c += NTHREADS) {
+    const int r = c / CPR;
+    const int dc = (c % CPR) * 8;
+    const int row = row0 + r;
+    u16x8 v = (u16x8)(0);
+    if (row < T && dc < dim) v = *reinterpret_cast<const u16x8*>(g + (int64_t)row * row_stride + dc);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lds[(dc + e) * LDS_STRIDE + r] = v[e];
+  }
+}
+
+// Load the 8-element k-slot group of a transposed LDS tile for lane `half`
+// and k-step m: slots e=0..3 -> columns 16m+4*half+e, e=4..7 -> 16m+8+4*half+(e-4).
+// This matches the accumulator row order m = 8*(r/4) + 4*half + r%4 of the
+// first GEMM, so registers r = 8m..8m+7 of that GEMM are the B operand.
+__device__ __forceinline__ u16x8 load_tr_slots(const u16* row_ptr, int m, int half) {
+  const u16x4 lo = *reinterpret_cast<const u16x4*>(row_ptr + 16 * m + 4 * half);
+  const u16x4 hi = *reinterpret_cast<const u16x4*>(row_ptr + 16 * m + 8 + 4 * half);
+  return (u16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+}  // namespace lard

@@ -1,0 +1,30 @@
+// Stage B launcher: per-row KL given both LSE vectors (kernel_B.py:340-389).
+#include "stage_kernels.h"
+#include "stage_dispatch.h"
+
+namespace lard {
+
+template <int DPS>
+static hipError_t launch_kl(const RelArgs& a, int dpt, dim3 grid, hipStream_t stream) {
+  switch (dpt) {
+#define X(DP, unused) \
+  case DP: hipLaunchKernelGGL((row_kernel<MODE_KL, DPS, DP>), grid, dim3(kStageThreads), 0, stream, a); break;
+    LARD_DP_CASES(X, 0)
+#undef X
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_row_kl(const RelArgs& a, int dps, int dpt, hipStream_t stream) {
+  const dim3 grid((a.T + kStageRows - 1) / kStageRows, a.B * a.Hq);
+  switch (dps) {
+#define X(DP, unused) \
+  case DP: return launch_kl<DP>(a, dpt, grid, stream);
+    LARD_DP_CASES(X, 0)
+#undef X
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace lard

@@ -1,0 +1,109 @@
+"""CPU-side checks of the C ABI library and the host layer (no GPU needed).
+
+Nothing here launches a kernel: the library must load, bind every symbol the
+public header declares, and reject invalid arguments before touching the GPU.
+"""
+
+import ctypes
+import inspect
+import os
+
+import pytest
+import torch
+
+from linearard_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_header_symbol():
+    names = _lib.header_functions()
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header exactly"
+    L = _lib.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.lard_version().decode().startswith("linearard_amd")
+
+
+def test_abi_rejects_bad_arguments_without_a_gpu():
+    L = _lib.lib()
+    t = _lib.Tensor4()
+    t.data = 16
+    t.size[:] = [1, 2, 8, 24]
+    t.stride[:] = [384, 192, 24, 1]
+    t.dtype = 1
+    m = _lib.Mask()
+    rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
+    assert rc == -2 and b"supported set" in L.lard_last_error()
+    t.size[3] = 16
+    t.stride[:] = [256, 128, 16, 1]
+    t.dtype = 7
+    rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
+    assert rc == -2 and b"fp16/bf16" in L.lard_last_error()
+    t.dtype = 0
+    t.stride[3] = 2
+    rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
+    assert rc == -1 and b"last-dim stride" in L.lard_last_error()
+    t.stride[3] = 1
+    t.data = 8  # misaligned
+    rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
+    assert rc == -2 and b"aligned" in L.lard_last_error()
+    t.data = 16
+    m.kind = 9
+    rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
+    assert rc == -1 and b"attn_mask dtype" in L.lard_last_error()
+    m.kind = 0
+    rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, float("nan"), 64, None)
+    assert rc == -1 and b"sm_scale" in L.lard_last_error()
+    assert L.lard_kl_forward_workspace_bytes(2, 3, 5) == 2 * 3 * 5 * 4
+    assert L.lard_kl_forward_workspace_bytes(0, 3, 5) == 0
+
+
+def test_python_wrappers_reject_cpu_tensors():
+    from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
+
+    x = torch.zeros((1, 2, 8, 16), dtype=torch.bfloat16)
+    l = torch.zeros((1, 2, 8))
+    with pytest.raises(AssertionError, match="q/k must be on CUDA"):
+        lse_stats(x, x)
+    with pytest.raises(AssertionError, match="Q/K must be on CUDA"):
+        kl_forward(x, x, l, x, x, l)
+    with pytest.raises(AssertionError, match="Q/K must be on CUDA"):
+        kl_backward(x, x, l, x, x, l)
+    with pytest.raises(AssertionError, match="q must be a torch.Tensor"):
+        lse_stats(None, x)
+
+
+def test_wrappers_contain_no_math():
+    """Equivalent of the reference's static_audit_wrapper (test_kernel_A.py:102-119):
+    all arithmetic lives in the HIP library, none in the Python wrappers."""
+    from linearard_amd.attention_KL import kernel_A, kernel_B, kernel_C
+
+    banned = ["matmul", "einsum", "softmax", "logsumexp", "exp(", "log(", "sum(", "max(", "mean(",
+              "reshape", "transpose"]
+    for fn in (kernel_A.lse_stats, kernel_B.kl_forward, kernel_C.kl_backward):
+        src = inspect.getsource(fn).lower()
+        for key in banned:
+            assert key not in src, f"{fn.__name__} contains {key}"
+
+
+def test_no_runtime_compilation_fixed_instantiation_table():
+    """The reference counts Triton JIT specialisations (test_kernel_A.py:127-203);
+    here every kernel is compiled ahead of time, so the library's kernel table is
+    fixed: 5 LSE + 25 KL + 25 dq + 25 dk instantiations (padded D in 16..256)."""
+    path = os.path.join(ROOT, "linearard_amd", "csrc")
+    srcs = [f for f in os.listdir(path) if f.endswith(".hip")]
+    text = "".join(open(os.path.join(path, f)).read() for f in srcs)
+    assert "hiprtc" not in text.lower()
+    assert text.count("LARD_DP_CASES(X, 0)") >= 7
+
+
+def test_drop_in_shim_names():
+    from kernels.attention_KL import kernel_A, kernel_B, kernel_C
+    from kernels.attention_KL.integration import AttnKLAlignFn, attn_kl_align
+
+    assert kernel_A.lse_stats_triton is kernel_A.lse_stats
+    assert kernel_B.kl_forward_triton is kernel_B.kl_forward
+    assert kernel_C.kl_backward_triton is kernel_C.kl_backward
+    assert kernel_A.SUPPORTED_HEAD_DIMS == (8, 16, 32, 64, 128, 256)
+    assert callable(attn_kl_align) and issubclass(AttnKLAlignFn, torch.autograd.Function)
