@@ -1,0 +1,211 @@
+"""Benchmark of the attention-relation KL hot path on one MI355X.
+
+One step = one fwd+bwd of ``attn_kl_align(x_s, x_s, x_t, x_t, causal=True)``
+(the train.py self-relation call, train.py:380-402) at BASELINE config 4:
+B=1, H=32, n=32768, d=128, bf16, with a RoPE teacher (positions p) and a
+position-interpolated student (positions p/8) built from the same pre-RoPE
+Gaussian vectors.  Inputs are generated on the CPU with a seeded
+torch.Generator and are resident in HBM before timing starts.
+
+Printed metric: relation-tokens/s (one relation-token = one (b, h, i) row,
+train.py:404), whole job.  Extra fields carry TFLOP/s against the
+algorithmic 12*d*P flop count, the roofline of the dominant kernel (timed
+live with HIP events on the launch stream), peak HBM, and a CPU baseline:
+the oracle's linear-memory float32 restatement run on this host for one
+(b, h) relation, scaled to the same unit.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg4]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+MI355X_BF16_DENSE_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk/CU
+MI355X_HBM_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (B, H, n, d, student position scale, rope base)
+    "cfg4": (1, 32, 32768, 128, 8.0, 10000.0),
+    "cfg2": (1, 32, 4096, 128, 8.0, 10000.0),
+    "small": (1, 4, 2048, 128, 8.0, 10000.0),
+}
+
+
+def rope_pair(B, H, n, d, pos_scale, base, seed=0, outliers=4):
+    """Teacher/student pair: the same pre-RoPE vectors rotated at positions p
+    (teacher) and p / pos_scale (student), HF rotate_half layout."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randn((B, H, n, d), generator=g, dtype=torch.float32)
+    if outliers:
+        idx = torch.randperm(d, generator=g)[:outliers]
+        v[..., idx] *= 20.0 / math.sqrt(d)  # a few large channels; keeps logits O(10)
+    inv_freq = base ** (-torch.arange(0, d, 2, dtype=torch.float64) / d)
+    pos = torch.arange(n, dtype=torch.float64)
+
+    def rotate(p):
+        ang = torch.outer(p, inv_freq)
+        cos = torch.cat([ang.cos(), ang.cos()], -1).float()
+        sin = torch.cat([ang.sin(), ang.sin()], -1).float()
+        x1, x2 = v[..., : d // 2], v[..., d // 2:]
+        rot = torch.cat([-x2, x1], -1)
+        return (v * cos + rot * sin).to(torch.bfloat16)
+
+    return rotate(pos / pos_scale), rotate(pos)  # student, teacher
+
+
+def algorithmic_flops(B, H, n, d):
+    pairs = n * (n + 1) // 2
+    return 12 * d * pairs * B * H
+
+
+def cpu_baseline(n, d, relations):
+    """Time the oracle's chunked float32 fwd+bwd for ONE (b, h) relation."""
+    import numpy as np
+
+    from oracle import attn_kl as O
+
+    rng = np.random.default_rng(1)
+    xt = rng.standard_normal((n, d)).astype(np.float32)
+    xs = xt + 0.1 * rng.standard_normal((n, d)).astype(np.float32)
+    t0 = time.perf_counter()
+    O.self_relation_chunked(xs, xt, True, 1 / math.sqrt(d), 1 / math.sqrt(d), chunk=512, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    threads = os.environ.get("OMP_NUM_THREADS") or str(os.cpu_count())
+    return {
+        "value": n / dt,
+        "unit": "relation-tokens/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"1 of {relations} (b,h) relations at n={n}, d={d}, causal, fwd+bwd, float32 numpy "
+                  f"(oracle.attn_kl.self_relation_chunked), {dt:.1f} s; host {platform.processor() or platform.machine()}",
+        "tflops": 12 * d * (n * (n + 1) // 2) / dt / 1e12,
+    }
+
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg4", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; the multi-GPU sharding is a design note "
+                                   "(DESIGN.md), not a launched path", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    from linearard_amd.attention_KL import attn_kl_align
+
+    B, H, n, d, pos_scale, base = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    xs_cpu, xt_cpu = rope_pair(B, H, n, d, pos_scale, base)
+    x_s = xs_cpu.to(dev).requires_grad_(True)
+    x_t = xt_cpu.to(dev)
+    del xs_cpu, xt_cpu
+    scale = d ** -0.5
+    stream = torch.cuda.current_stream(dev)
+
+    ev = {"fwd": [], "bwd": []}
+    marks = {}
+
+    def on_loss_grad(g):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(stream)
+        marks["b0"] = e
+        return g
+
+    def on_input_grad(g):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(stream)
+        marks["b1"] = e
+        return g
+
+    x_s.register_hook(on_input_grad)
+
+    def step(timed):
+        x_s.grad = None
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        loss = attn_kl_align(x_s, x_s, x_t, x_t, attn_mask=None, causal=True, sm_scale_s=scale, sm_scale_t=scale)
+        e1.record(stream)
+        loss.register_hook(on_loss_grad)
+        loss.backward()
+        if timed:
+            ev["fwd"].append((e0, e1))
+            ev["bwd"].append((marks["b0"], marks["b1"]))
+        return loss
+
+    base_mem = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    peak = torch.cuda.max_memory_allocated(dev) - base_mem
+
+    fwd_ms = sum(a.elapsed_time(b) for a, b in ev["fwd"]) / len(ev["fwd"])
+    bwd_ms = sum(a.elapsed_time(b) for a, b in ev["bwd"]) / len(ev["bwd"])
+    ms = elapsed / args.steps * 1e3
+    flops = algorithmic_flops(B, H, n, d)
+    rows = B * H * n
+    # Each phase is credited half of the 12 d P algorithmic flops: the forward
+    # owns S_s, S_t (4dP) plus the row-side D.X product (2dP); the backward
+    # owns the S_s, S_t recompute (4dP) plus D^T.X (2dP).
+    dom_name, dom_ms = ("backward", bwd_ms) if bwd_ms >= fwd_ms else ("forward", fwd_ms)
+    achieved = (flops / 2) / (dom_ms * 1e-3) / 1e12
+
+    out = {
+        "metric": "attention-KL fwd+bwd relation-tokens/sec at n=32K, d=128",
+        "value": rows / (ms * 1e-3),
+        "unit": "relation-tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian pre-RoPE vectors, RoPE teacher at p, student at p/8)",
+        "config": {"workload": f"{args.config}: self-relation Q/Q KL fwd+bwd, B={B}, H={H}, n={n}, d={d}, causal",
+                   "B": B, "H": H, "n": n, "d": d, "causal": True},
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS,
+        "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
+        "peak_hbm_bytes": int(peak),
+        "loss": float(loss.item()),
+        "roofline": {"bound": "mfma", "kernel": dom_name, "achieved": achieved,
+                     "peak": MI355X_BF16_DENSE_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / MI355X_BF16_DENSE_TFLOPS, "traffic": None},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(n, d, B * H)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -47,12 +47,11 @@ def check_scale(value, default_dim: int, name: str) -> float:
     return float(value)
 
 
-def check_two_sided(qs, ks, lse_s, qt, kt, lse_t):
-    """kernel_B.py:262-309 / kernel_C.py:307-354."""
-    for t, n in ((qs, "qs"), (ks, "ks"), (qt, "qt"), (kt, "kt"), (lse_s, "lse_s"), (lse_t, "lse_t")):
+def check_relations(qs, ks, qt, kt):
+    """The q/k preconditions of kernel_B.py:262-309 (no lse involved)."""
+    for t, n in ((qs, "qs"), (ks, "ks"), (qt, "qt"), (kt, "kt")):
         require(isinstance(t, torch.Tensor), f"{n} must be a torch.Tensor")
     require(qs.is_cuda and ks.is_cuda and qt.is_cuda and kt.is_cuda, "Q/K must be on CUDA")
-    require(lse_s.is_cuda and lse_t.is_cuda, "lse must be on CUDA")
     require(qs.dtype in _HALF_TYPES, "qs dtype supports only fp16/bf16")
     require(ks.dtype in _HALF_TYPES, "ks dtype supports only fp16/bf16")
     require(qt.dtype in _HALF_TYPES, "qt dtype supports only fp16/bf16")
@@ -67,23 +66,34 @@ def check_two_sided(qs, ks, lse_s, qt, kt, lse_t):
     require(qt.shape[0] == kt.shape[0], "qt/kt B must match")
     require(qt.shape[2] == kt.shape[2], "qt/kt T must match")
     require(qt.shape[3] == kt.shape[3], "qt/kt Dt must match")
-    require(lse_s.ndim == 3 and lse_t.ndim == 3, "lse shape must be [B,H,T]")
     require(qs.is_contiguous() and ks.is_contiguous(), "qs/ks must be contiguous")
     require(qt.is_contiguous() and kt.is_contiguous(), "qt/kt must be contiguous")
     require(qs.stride(-1) == 1 and ks.stride(-1) == 1, "qs/ks last-dim stride must be 1")
     require(qt.stride(-1) == 1 and kt.stride(-1) == 1, "qt/kt last-dim stride must be 1")
-    require(lse_s.dtype == torch.float32 and lse_t.dtype == torch.float32, "lse must be float32")
-    require(lse_s.is_contiguous() and lse_t.is_contiguous(), "lse must be contiguous")
-    require(lse_s.stride(-1) == 1 and lse_t.stride(-1) == 1, "lse last-dim stride must be 1")
     B, Hq, T, Ds = qs.shape
     B2, Hq2, T2, Dt = qt.shape
     Hkv_s = ks.shape[1]
     Hkv_t = kt.shape[1]
-    require((B, Hq, T) == tuple(lse_s.shape), "lse_s shape must match [B,Hq,T]")
-    require((B2, Hq2, T2) == tuple(lse_t.shape), "lse_t shape must match [B,Hq,T]")
     require((B, Hq, T) == (B2, Hq2, T2), "student/teacher B/Hq/T must align")
     require(Hkv_s > 0 and Hq % Hkv_s == 0, "Hq must be divisible by Hkv_s")
     require(Hkv_t > 0 and Hq % Hkv_t == 0, "Hq must be divisible by Hkv_t")
     require(Ds in SUPPORTED_HEAD_DIMS, "Ds is not in the supported set")
     require(Dt in SUPPORTED_HEAD_DIMS, "Dt is not in the supported set")
     return B, Hq, T, Ds, Dt
+
+
+def check_two_sided(qs, ks, lse_s, qt, kt, lse_t):
+    """kernel_B.py:262-309 / kernel_C.py:307-354."""
+    for t, n in ((qs, "qs"), (ks, "ks"), (qt, "qt"), (kt, "kt"), (lse_s, "lse_s"), (lse_t, "lse_t")):
+        require(isinstance(t, torch.Tensor), f"{n} must be a torch.Tensor")
+    require(qs.is_cuda and ks.is_cuda and qt.is_cuda and kt.is_cuda, "Q/K must be on CUDA")
+    require(lse_s.is_cuda and lse_t.is_cuda, "lse must be on CUDA")
+    require(lse_s.ndim == 3 and lse_t.ndim == 3, "lse shape must be [B,H,T]")
+    require(lse_s.dtype == torch.float32 and lse_t.dtype == torch.float32, "lse must be float32")
+    require(lse_s.is_contiguous() and lse_t.is_contiguous(), "lse must be contiguous")
+    require(lse_s.stride(-1) == 1 and lse_t.stride(-1) == 1, "lse last-dim stride must be 1")
+    dims = check_relations(qs, ks, qt, kt)
+    B, Hq, T = dims[:3]
+    require((B, Hq, T) == tuple(lse_s.shape), "lse_s shape must match [B,Hq,T]")
+    require((B, Hq, T) == tuple(lse_t.shape), "lse_t shape must match [B,Hq,T]")
+    return dims

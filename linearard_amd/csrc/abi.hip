@@ -12,7 +12,7 @@
 #include <string>
 
 #include "../../include/linearard_amd.h"
-#include "stage_kernels.h"
+#include "fused_kernels.h"
 
 namespace {
 
@@ -228,6 +228,107 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
   const int dps = padded_dim(qs->size[3]), dpt = padded_dim(qt->size[3]);
   if ((rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "kl_backward dq launch")) != LARD_OK) return rc;
   return hip_status(lard::launch_col_dk(a, dps, dpt, st), "kl_backward dk launch");
+}
+
+size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
+  return lard_kl_forward_workspace_bytes(batch, heads, seq_len);
+}
+
+int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+                         const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
+                         float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out, float* dq_out,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
+  if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
+  if (qs->size[0] != qt->size[0] || qs->size[1] != qt->size[1] || qs->size[2] != qt->size[2])
+    return fail(LARD_ERR_INVALID_ARGUMENT, "student/teacher B/Hq/T must align");
+  if ((rc = check_mask(mask, qs->size[0], qs->size[2])) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_s, "sm_scale_s")) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_t, "sm_scale_t")) != LARD_OK) return rc;
+  if (loss_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "loss_out must not be NULL");
+  const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
+  const int64_t n = B * Hq * T;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n > 0) {
+    if (lse_s_out == nullptr || lse_t_out == nullptr)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "lse outputs must not be NULL");
+    if ((rc = check_grid(B * Hq)) != LARD_OK) return rc;
+    if (workspace == nullptr || workspace_bytes < lard_attn_kl_forward_workspace_bytes(B, Hq, T))
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes",
+                  lard_attn_kl_forward_workspace_bytes(B, Hq, T));
+    const int ds = (int)qs->size[3], dt = (int)qt->size[3];
+    if (lard::fused_fwd_supported(ds, dt, qs->dtype == qt->dtype)) {
+      lard::FusedArgs f{};
+      fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
+      fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
+      fill_common(f.r, B, Hq, T, mask, causal);
+      f.lse_s_out = lse_s_out;
+      f.lse_t_out = lse_t_out;
+      f.row_out = static_cast<float*>(workspace);
+      const bool grad_in_pass = dq_out != nullptr && lard::fused_fwd_grad_supported(ds);
+      f.dq_out = grad_in_pass ? dq_out : nullptr;
+      if ((rc = hip_status(lard::launch_fused_fwd(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, grad_in_pass, st),
+                           "attn_kl_forward fused launch")) != LARD_OK)
+        return rc;
+      if (dq_out != nullptr && !grad_in_pass) {  // stage C row side from the fused LSEs
+        lard::RelArgs a = f.r;
+        a.lse_s_in = lse_s_out;
+        a.lse_t_in = lse_t_out;
+        a.dq_out = dq_out;
+        if ((rc = hip_status(lard::launch_row_dq(a, padded_dim(ds), padded_dim(dt), st), "attn_kl_forward dq launch")) !=
+            LARD_OK)
+          return rc;
+      }
+    } else {
+      // Stage A twice, stage B, and (for autograd) the stage C row side.
+      if ((rc = lard_lse_stats(qs, ks, mask, causal, sm_scale_s, lse_s_out, stream)) != LARD_OK) return rc;
+      if ((rc = lard_lse_stats(qt, kt, mask, causal, sm_scale_t, lse_t_out, stream)) != LARD_OK) return rc;
+      lard::RelArgs a{};
+      fill_side(a.s, qs, ks, Hq, sm_scale_s);
+      fill_side(a.t, qt, kt, Hq, sm_scale_t);
+      fill_common(a, B, Hq, T, mask, causal);
+      a.lse_s_in = lse_s_out;
+      a.lse_t_in = lse_t_out;
+      a.row_out = static_cast<float*>(workspace);
+      a.dq_out = dq_out;
+      const int dps = padded_dim(ds), dpt = padded_dim(dt);
+      if ((rc = hip_status(lard::launch_row_kl(a, dps, dpt, st), "attn_kl_forward kl launch")) != LARD_OK) return rc;
+      if (dq_out != nullptr &&
+          (rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "attn_kl_forward dq launch")) != LARD_OK)
+        return rc;
+    }
+  }
+  return hip_status(lard::launch_reduce_sum(static_cast<const float*>(workspace), n, loss_out, st),
+                    "attn_kl_forward reduce launch");
+}
+
+int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
+                          const lard_tensor4* kt, const float* lse_t, const lard_mask* mask, int causal,
+                          float sm_scale_s, float sm_scale_t, const float* dq_row, const float* dloss,
+                          int self_relation, float* dk_out, void* stream) {
+  int rc;
+  if ((rc = check_two_sided(qs, ks, lse_s, qt, kt, lse_t, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
+  if (B * Hq * T == 0) return ok();
+  if (dk_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "dk_out must not be NULL");
+  if (self_relation) {
+    if (dq_row == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "self relation needs the forward's dq_row");
+    if (ks->size[1] != Hq || qs->data != ks->data)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "self relation needs q and k to be the same tensor");
+  }
+  lard::RelArgs a{};
+  fill_side(a.s, qs, ks, Hq, sm_scale_s);
+  fill_side(a.t, qt, kt, Hq, sm_scale_t);
+  fill_common(a, B, Hq, T, mask, causal);
+  a.lse_s_in = lse_s;
+  a.lse_t_in = lse_t;
+  a.dk_out = dk_out;
+  a.dk_add = self_relation ? dq_row : nullptr;
+  a.dscale = dloss;
+  return hip_status(lard::launch_col_dk(a, padded_dim(qs->size[3]), padded_dim(qt->size[3]),
+                                        static_cast<hipStream_t>(stream)),
+                    "attn_kl_backward dk launch");
 }
 
 }  // extern "C"

@@ -389,15 +389,19 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
   }
 
   if (in_range) {
-    float* out = a.dk_out + ((int64_t)bg * T + my_j) * a.s.dim;
+    const int64_t off = ((int64_t)bg * T + my_j) * a.s.dim;
+    float* out = a.dk_out + off;
     const float f = a.s.scale;
+    const float mult = a.dscale != nullptr ? *a.dscale : 1.f;  // chain rule (integration.py:63-64)
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         const int d0 = 32 * db + 8 * gq + 4 * half;
         if (d0 < a.s.dim) {
-          const f32x4 v = {dk[db][4 * gq] * f, dk[db][4 * gq + 1] * f, dk[db][4 * gq + 2] * f, dk[db][4 * gq + 3] * f};
+          f32x4 v = {dk[db][4 * gq] * f, dk[db][4 * gq + 1] * f, dk[db][4 * gq + 2] * f, dk[db][4 * gq + 3] * f};
+          if (a.dk_add != nullptr) v += *reinterpret_cast<const f32x4*>(a.dk_add + off + d0);
+          if (a.dscale != nullptr) v *= mult;
           *reinterpret_cast<f32x4*>(out + d0) = v;
         }
       }
