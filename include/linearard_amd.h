@@ -102,37 +102,43 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
                      const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
                      float* dq_out, float* dk_out, void* stream);
 
-/* Workspace needed by lard_attn_kl_forward (bytes). */
+/* Workspace needed by lard_attn_kl_forward (bytes): the per-row KL terms. */
 size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len);
 
 /*
- * Autograd forward -- replaces AttnKLAlignFn.forward (integration.py:8-45),
- * i.e. stage A for both relations followed by stage B.
- * Writes lse_s_out / lse_t_out [B, Hq, T] (as stage A), loss_out[0] (as
- * stage B) and, when dq_out is not NULL, the row-side gradient
- * dq_out[B, Hq, T, Ds] = sm_scale_s (P_s - P_t) K_s (float32), which is the
- * dq of stage C computed in the same pass.  When Ds == Dt <= 128 and both
- * relations share a dtype this is one fused pass over the key tiles; other
- * shapes run the stage kernels.
+ * Autograd forward -- replaces AttnKLAlignFn.forward (integration.py:8-45):
+ * stage A for both relations followed by stage B, in one pass over the key
+ * tiles when Ds == Dt and both relations share a dtype (the stage kernels
+ * otherwise).  Writes lse_s_out / lse_t_out [B, Hq, T] (as stage A; the
+ * backward's input) and loss_out[0] (as stage B, a deterministic sum).
  */
 int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
                          const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
                          float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
-                         float* dq_out, void* workspace, size_t workspace_bytes, void* stream);
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by lard_attn_kl_backward (bytes): transposed copies of ks
+ * and (unless self_relation) qs. */
+size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,
+                                             int64_t head_dim, int self_relation);
 
 /*
- * Autograd backward -- replaces AttnKLAlignFn.backward (integration.py:48-67)
- * given the forward's LSE vectors.  Writes
- *   dk_out[B, Hkv_s, T, Ds] = (sm_scale_s sum_{h in group} D^T Q_s + add) * dloss
- * where add = dq_row when self_relation != 0 (q and k are the same tensor,
- * the train.py call; dk_out is then the full gradient of that tensor) and 0
- * otherwise.  dloss is a device float32 scalar or NULL (1).
+ * Autograd backward -- replaces AttnKLAlignFn.backward (integration.py:48-67):
+ * stage C from the forward's LSE vectors followed by the chain rule with
+ * dloss (a device float32 scalar, or NULL for 1).  Writes
+ *   dq_out[B, Hq, T, Ds]    = dloss * sm_scale_s D K_s
+ *   dk_out[B, Hkv_s, T, Ds] = dloss * sm_scale_s sum_{h in group} D^T Q_s
+ * with D = P_s - P_t cast to the student dtype (kernel_C.py:232-233).  With
+ * self_relation != 0 (q and k are the same tensor, the train.py call) the
+ * sum dq + dk -- the whole gradient of that tensor -- goes to dk_out and
+ * dq_out is not used.  Both sides have one owning workgroup per row / key
+ * tile: no atomics, bitwise deterministic.
  */
 int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s,
                           const lard_tensor4* qt, const lard_tensor4* kt, const float* lse_t,
                           const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
-                          const float* dq_row, const float* dloss, int self_relation, float* dk_out,
-                          void* stream);
+                          const float* dloss, int self_relation, float* dq_out, float* dk_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

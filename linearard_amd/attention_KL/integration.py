@@ -6,14 +6,14 @@ KL(P_t || P_s), P_x = softmax of the (masked, causal) relation logits
 sm_scale_x * q_x . k_x.  Gradients flow to qs and ks only; the teacher,
 mask, causal flag and scales get None (integration.py:67).
 
-Forward (``lard_attn_kl_forward``): one pass over the key tiles yields both
-LSE vectors, the per-row KL and, when a gradient is needed, the row-side
-gradient dq = sm_scale_s (P_s - P_t) K_s.  Backward
-(``lard_attn_kl_backward``): one column-owner pass yields
-dk = sm_scale_s sum_h D^T Q_s.  For the train.py call ``attn_kl_align(x, x,
-y, y)`` (q is k), the backward adds the saved dq and returns the whole
-gradient of ``x`` as the first output (and None for the second), so autograd
-accumulates it once.
+Forward (``lard_attn_kl_forward``): stage A for both relations and stage B in
+one pass over the key tiles; only the two LSE vectors are saved (O(n), as in
+integration.py:40).  Backward (``lard_attn_kl_backward``): stage C as a
+row-owner pass (dq) and a column-owner pass (dk), both with D = P_s - P_t cast
+to the input dtype before the product like kernel_C.py:233.  For the train.py
+call ``attn_kl_align(x, x, y, y)`` (q is k) the library sums dq + dk in place
+and the Function returns that whole gradient of ``x`` once (None for the
+second input) instead of two float32 tensors for autograd to add.
 """
 
 from __future__ import annotations
@@ -28,35 +28,35 @@ from ._checks import check_mask, check_relations, check_scale
 __all__ = ["AttnKLAlignFn", "attn_kl_align"]
 
 
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty((nbytes if nbytes > 0 else 1,), device=device, dtype=torch.uint8)
+
+
 class AttnKLAlignFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, qs, ks, qt, kt, attn_mask, causal: bool, sm_scale_s, sm_scale_t):
-        """integration.py:8-45 (stage A x2 + stage B), fused in the library."""
+        """integration.py:8-45: stage A x2 + stage B."""
         B, Hq, T, Ds, Dt = check_relations(qs, ks, qt, kt)
         attn_mask = check_mask(attn_mask, qs.device, B, T)
         ss = check_scale(sm_scale_s, Ds, "sm_scale_s")
         st = check_scale(sm_scale_t, Dt, "sm_scale_t")
-        want_grad = bool(ctx.needs_input_grad[0] or ctx.needs_input_grad[1])
 
         L = _lib.lib()
         dev = qs.device
         lse_s = torch.empty((B, Hq, T), device=dev, dtype=torch.float32)
         lse_t = torch.empty((B, Hq, T), device=dev, dtype=torch.float32)
         loss = torch.empty((), device=dev, dtype=torch.float32)
-        dq_row = torch.empty((B, Hq, T, Ds), device=dev, dtype=torch.float32) if want_grad else None
         ws_bytes = L.lard_attn_kl_forward_workspace_bytes(B, Hq, T)
-        ws = torch.empty((ws_bytes // 4 if ws_bytes >= 4 else 1,), device=dev, dtype=torch.float32)
+        ws = _workspace(ws_bytes, dev)
         d = [_lib.tensor4(x) for x in (qs, ks, qt, kt)]
         md = _lib.mask_desc(attn_mask)
         rc = L.lard_attn_kl_forward(ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), ctypes.byref(d[3]),
                                     ctypes.byref(md), int(bool(causal)), ss, st, lse_s.data_ptr(), lse_t.data_ptr(),
-                                    loss.data_ptr(), dq_row.data_ptr() if dq_row is not None else None,
-                                    ws.data_ptr(), ws_bytes, _lib.stream_of(qs))
+                                    loss.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(qs))
         _lib.check(rc, "lard_attn_kl_forward")
 
         saved_mask = attn_mask if attn_mask is not None else torch.empty(0, device=dev)
-        saved_dq = dq_row if dq_row is not None else torch.empty(0, device=dev)
-        ctx.save_for_backward(qs, ks, lse_s, qt, kt, lse_t, saved_mask, saved_dq)
+        ctx.save_for_backward(qs, ks, lse_s, qt, kt, lse_t, saved_mask)
         ctx.has_mask = attn_mask is not None
         ctx.causal = bool(causal)
         ctx.sm_scale_s = ss
@@ -67,21 +67,27 @@ class AttnKLAlignFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dloss):
         """integration.py:48-67: stage C and the chain rule with dloss."""
-        qs, ks, lse_s, qt, kt, lse_t, saved_mask, dq_row = ctx.saved_tensors
+        qs, ks, lse_s, qt, kt, lse_t, saved_mask = ctx.saved_tensors
         attn_mask = saved_mask if ctx.has_mask else None
         dloss = dloss.detach().to(torch.float32).contiguous()
         B, Hq, T, Ds = qs.shape
-        dk = torch.empty((B, ks.shape[1], T, Ds), device=qs.device, dtype=torch.float32)
+        self_rel = ctx.self_relation
+        dev = qs.device
+        dk = torch.empty((B, ks.shape[1], T, Ds), device=dev, dtype=torch.float32)
+        dq = None if self_rel else torch.empty((B, Hq, T, Ds), device=dev, dtype=torch.float32)
+        L = _lib.lib()
+        ws_bytes = L.lard_attn_kl_backward_workspace_bytes(B, Hq, ks.shape[1], T, Ds, int(self_rel))
+        ws = _workspace(ws_bytes, dev)
         d = [_lib.tensor4(x) for x in (qs, ks, qt, kt)]
         md = _lib.mask_desc(attn_mask)
-        rc = _lib.lib().lard_attn_kl_backward(
+        rc = L.lard_attn_kl_backward(
             ctypes.byref(d[0]), ctypes.byref(d[1]), lse_s.data_ptr(), ctypes.byref(d[2]), ctypes.byref(d[3]),
-            lse_t.data_ptr(), ctypes.byref(md), int(ctx.causal), ctx.sm_scale_s, ctx.sm_scale_t,
-            dq_row.data_ptr(), dloss.data_ptr(), int(ctx.self_relation), dk.data_ptr(), _lib.stream_of(qs))
+            lse_t.data_ptr(), ctypes.byref(md), int(ctx.causal), ctx.sm_scale_s, ctx.sm_scale_t, dloss.data_ptr(),
+            int(self_rel), None if dq is None else dq.data_ptr(), dk.data_ptr(), ws.data_ptr(), ws_bytes,
+            _lib.stream_of(qs))
         _lib.check(rc, "lard_attn_kl_backward")
-        if ctx.self_relation:
+        if self_rel:
             return dk, None, None, None, None, None, None, None
-        dq = dq_row * dloss
         return dq, dk, None, None, None, None, None, None
 
 

@@ -12,7 +12,7 @@
 #include <string>
 
 #include "../../include/linearard_amd.h"
-#include "fused_kernels.h"
+#include "hot_kernels.h"
 
 namespace {
 
@@ -230,14 +230,22 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
   return hip_status(lard::launch_col_dk(a, dps, dpt, st), "kl_backward dk launch");
 }
 
+static int64_t padded_len(int64_t T) { return (T + lard::kTile - 1) / lard::kTile * lard::kTile; }
+
+static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+static size_t transposed_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
+  return align256((size_t)(batch * heads * head_dim * padded_len(seq_len)) * sizeof(uint16_t));
+}
+
 size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
   return lard_kl_forward_workspace_bytes(batch, heads, seq_len);
 }
 
 int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
                          const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
-                         float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out, float* dq_out,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+                         float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out, void* workspace,
+                         size_t workspace_bytes, void* stream) {
   int rc;
   if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
   if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
@@ -254,34 +262,33 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
     if (lse_s_out == nullptr || lse_t_out == nullptr)
       return fail(LARD_ERR_INVALID_ARGUMENT, "lse outputs must not be NULL");
     if ((rc = check_grid(B * Hq)) != LARD_OK) return rc;
-    if (workspace == nullptr || workspace_bytes < lard_attn_kl_forward_workspace_bytes(B, Hq, T))
-      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes",
-                  lard_attn_kl_forward_workspace_bytes(B, Hq, T));
+    const size_t need = lard_attn_kl_forward_workspace_bytes(B, Hq, T);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
     const int ds = (int)qs->size[3], dt = (int)qt->size[3];
-    if (lard::fused_fwd_supported(ds, dt, qs->dtype == qt->dtype)) {
-      lard::FusedArgs f{};
+    const bool same = qs->dtype == qt->dtype;
+    const bool bf = qs->dtype == LARD_DTYPE_BF16;
+    if (lard::hot_supported(ds, dt, same) || lard::fused_fwd_supported(ds, dt, same)) {
+      lard::HotArgs f{};
       fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
       fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
       fill_common(f.r, B, Hq, T, mask, causal);
       f.lse_s_out = lse_s_out;
       f.lse_t_out = lse_t_out;
       f.row_out = static_cast<float*>(workspace);
-      const bool grad_in_pass = dq_out != nullptr && lard::fused_fwd_grad_supported(ds);
-      f.dq_out = grad_in_pass ? dq_out : nullptr;
-      if ((rc = hip_status(lard::launch_fused_fwd(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, grad_in_pass, st),
-                           "attn_kl_forward fused launch")) != LARD_OK)
-        return rc;
-      if (dq_out != nullptr && !grad_in_pass) {  // stage C row side from the fused LSEs
-        lard::RelArgs a = f.r;
-        a.lse_s_in = lse_s_out;
-        a.lse_t_in = lse_t_out;
-        a.dq_out = dq_out;
-        if ((rc = hip_status(lard::launch_row_dq(a, padded_dim(ds), padded_dim(dt), st), "attn_kl_forward dq launch")) !=
-            LARD_OK)
-          return rc;
+      if (lard::hot_supported(ds, dt, same)) {
+        rc = hip_status(lard::launch_hot_fwd(f, padded_dim(ds), bf, st), "attn_kl_forward launch");
+      } else {
+        lard::FusedArgs g{};
+        g.r = f.r;
+        g.lse_s_out = lse_s_out;
+        g.lse_t_out = lse_t_out;
+        g.row_out = f.row_out;
+        rc = hip_status(lard::launch_fused_fwd(g, padded_dim(ds), bf, st), "attn_kl_forward fused launch");
       }
+      if (rc != LARD_OK) return rc;
     } else {
-      // Stage A twice, stage B, and (for autograd) the stage C row side.
+      // Stage A twice, then stage B (the reference's own composition).
       if ((rc = lard_lse_stats(qs, ks, mask, causal, sm_scale_s, lse_s_out, stream)) != LARD_OK) return rc;
       if ((rc = lard_lse_stats(qt, kt, mask, causal, sm_scale_t, lse_t_out, stream)) != LARD_OK) return rc;
       lard::RelArgs a{};
@@ -291,11 +298,8 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
       a.lse_s_in = lse_s_out;
       a.lse_t_in = lse_t_out;
       a.row_out = static_cast<float*>(workspace);
-      a.dq_out = dq_out;
-      const int dps = padded_dim(ds), dpt = padded_dim(dt);
-      if ((rc = hip_status(lard::launch_row_kl(a, dps, dpt, st), "attn_kl_forward kl launch")) != LARD_OK) return rc;
-      if (dq_out != nullptr &&
-          (rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "attn_kl_forward dq launch")) != LARD_OK)
+      if ((rc = hip_status(lard::launch_row_kl(a, padded_dim(ds), padded_dim(dt), st), "attn_kl_forward kl launch")) !=
+          LARD_OK)
         return rc;
     }
   }
@@ -303,32 +307,84 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
                     "attn_kl_forward reduce launch");
 }
 
+size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,
+                                             int64_t head_dim, int self_relation) {
+  if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  const size_t kt = transposed_bytes(batch, kv_heads, seq_len, head_dim);
+  return self_relation ? kt : kt + transposed_bytes(batch, heads, seq_len, head_dim);
+}
+
 int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
                           const lard_tensor4* kt, const float* lse_t, const lard_mask* mask, int causal,
-                          float sm_scale_s, float sm_scale_t, const float* dq_row, const float* dloss,
-                          int self_relation, float* dk_out, void* stream) {
+                          float sm_scale_s, float sm_scale_t, const float* dloss, int self_relation, float* dq_out,
+                          float* dk_out, void* workspace, size_t workspace_bytes, void* stream) {
   int rc;
   if ((rc = check_two_sided(qs, ks, lse_s, qt, kt, lse_t, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
   const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
   if (B * Hq * T == 0) return ok();
   if (dk_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "dk_out must not be NULL");
   if (self_relation) {
-    if (dq_row == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "self relation needs the forward's dq_row");
-    if (ks->size[1] != Hq || qs->data != ks->data)
+    if (ks->size[1] != Hq || qs->data != ks->data || qs->stride[0] != ks->stride[0] ||
+        qs->stride[1] != ks->stride[1] || qs->stride[2] != ks->stride[2])
       return fail(LARD_ERR_INVALID_ARGUMENT, "self relation needs q and k to be the same tensor");
+  } else if (dq_out == nullptr) {
+    return fail(LARD_ERR_INVALID_ARGUMENT, "dq_out must not be NULL");
   }
+  // Row side first (into dk_out for a self relation), then the column side,
+  // which adds the row side in place and applies dloss once.
+  float* dq_dst = self_relation ? dk_out : dq_out;
   lard::RelArgs a{};
   fill_side(a.s, qs, ks, Hq, sm_scale_s);
   fill_side(a.t, qt, kt, Hq, sm_scale_t);
   fill_common(a, B, Hq, T, mask, causal);
   a.lse_s_in = lse_s;
   a.lse_t_in = lse_t;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int ds = (int)qs->size[3], dt = (int)qt->size[3];
+  if (lard::hot_supported(ds, dt, qs->dtype == qt->dtype)) {
+    const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+    const int Tp = (int)padded_len(T);
+    lard::u16* kT = static_cast<lard::u16*>(workspace);
+    lard::u16* qT = self_relation ? kT
+                                  : reinterpret_cast<lard::u16*>(static_cast<char*>(workspace) +
+                                                                 transposed_bytes(B, ks->size[1], T, ds));
+    if ((rc = hip_status(lard::launch_transpose_keys(static_cast<const lard::u16*>(ks->data), ks->stride[0],
+                                                     ks->stride[1], ks->stride[2], (int)B, (int)ks->size[1], (int)T,
+                                                     ds, Tp, kT, st),
+                         "attn_kl_backward transpose launch")) != LARD_OK)
+      return rc;
+    if (!self_relation &&
+        (rc = hip_status(lard::launch_transpose_keys(static_cast<const lard::u16*>(qs->data), qs->stride[0],
+                                                     qs->stride[1], qs->stride[2], (int)B, (int)Hq, (int)T, ds, Tp,
+                                                     qT, st),
+                         "attn_kl_backward transpose launch")) != LARD_OK)
+      return rc;
+    lard::HotArgs f{};
+    f.r = a;
+    f.Tp = Tp;
+    f.xT = kT;
+    f.dq_out = dq_dst;
+    f.r.dscale = self_relation ? nullptr : dloss;
+    if ((rc = hip_status(lard::launch_hot_dq(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, st),
+                         "attn_kl_backward dq launch")) != LARD_OK)
+      return rc;
+    f.xT = qT;
+    f.r.dk_out = dk_out;
+    f.r.dk_add = self_relation ? dk_out : nullptr;
+    f.r.dscale = dloss;
+    return hip_status(lard::launch_hot_bwd(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, st),
+                      "attn_kl_backward dk launch");
+  }
+  const int dps = padded_dim(ds), dpt = padded_dim(dt);
+  a.dq_out = dq_dst;
+  a.dscale = self_relation ? nullptr : dloss;
+  if ((rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "attn_kl_backward dq launch")) != LARD_OK) return rc;
   a.dk_out = dk_out;
-  a.dk_add = self_relation ? dq_row : nullptr;
+  a.dk_add = self_relation ? dk_out : nullptr;
   a.dscale = dloss;
-  return hip_status(lard::launch_col_dk(a, padded_dim(qs->size[3]), padded_dim(qt->size[3]),
-                                        static_cast<hipStream_t>(stream)),
-                    "attn_kl_backward dk launch");
+  return hip_status(lard::launch_col_dk(a, dps, dpt, st), "attn_kl_backward dk launch");
 }
 
 }  // extern "C"

@@ -6,23 +6,18 @@
 //   KL_i                    E_{p_t}[x_t - x_s] - lse_t + lse_s, accumulated online
 //                           (equal to sum_j p_t (l_t - l_s) of kernel_B.py:206-213
 //                           because sum_j p_t = 1 on every valid row),
-//   dq_i (optional)         sm_scale_s * (P_s K_s - P_t K_s)_i from two unnormalised
-//                           accumulators rescaled like an online softmax; this is
-//                           the row-side half of the stage C gradient
-//                           (kernel_C.py:236-239), so the backward only has to
-//                           produce the column-side half.
 //
-// Tile mapping is that of row_kernel: 4 waves x 32 query rows; S^T tiles keep
-// one query row per lane (pair), so row statistics are in-lane reductions plus
-// one cross-half exchange.  The P.K products take P straight from the
-// accumulator registers as the B operand (see load_tr_slots).
+// It serves the shapes the throughput kernels (hot_kernels.h) do not cover:
+// Ds == Dt == 256.  Tile mapping is that of row_kernel: 4 waves x 32 query
+// rows; S^T tiles keep one query row per lane (pair), so row statistics are
+// in-lane reductions plus one cross-half exchange.
 #pragma once
 
 #include "stage_kernels.h"
 
 namespace lard {
 
-template <int DP, bool BF, bool GRAD>
+template <int DP, bool BF>
 __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArgs f) {
   const RelArgs& a = f.r;
   constexpr int DPS = DP;  // student and teacher share the head dim and dtype on this path
@@ -32,12 +27,9 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
   constexpr int KT = DPT / 16;
   constexpr int SS = DPS + 8;
   constexpr int ST = DPT + 8;
-  constexpr int TRS = BN + 8;
-  constexpr int NDB = DPS >= 32 ? DPS / 32 : 1;
 
   __shared__ __attribute__((aligned(16))) u16 lks[BN * SS];
   __shared__ __attribute__((aligned(16))) u16 lkt[BN * ST];
-  __shared__ __attribute__((aligned(16))) u16 lkst[GRAD ? NDB * 32 * TRS : 8];
   __shared__ int lcol[BN];
 
   const int tid = threadIdx.x;
@@ -55,10 +47,6 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
   const int my_i = i0w + l32;
   const bool in_range = my_i < T;
   const bool row_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_i);
-  if constexpr (GRAD && DPS < 32) {
-    for (int c = tid; c < 32 * TRS; c += kStageThreads) lkst[c] = 0;
-  }
-
   u16x8 fq_s[KS];
   u16x8 fq_t[KT];
   {
@@ -80,12 +68,6 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
   float m_s = kNegInf, l_s = 0.f;
   float m_t = kNegInf, l_t = 0.f;
   float a_t = 0.f;  // sum_j p_t (x_t - x_s), same scaling as l_t
-  f32x16 u_s[GRAD ? NDB : 1], u_t[GRAD ? NDB : 1];
-#pragma unroll
-  for (int db = 0; db < (GRAD ? NDB : 1); ++db) {
-    u_s[db] = (f32x16)(0.f);
-    u_t[db] = (f32x16)(0.f);
-  }
 
   const int hs = h / a.s.group;
   const int ht = h / a.t.group;
@@ -101,8 +83,6 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
     __syncthreads();
     stage_rows<BN, DPS, SS, kStageThreads>(lks, ks_base, a.s.k_st, j0, T, a.s.dim, tid);
     stage_rows<BN, DPT, ST, kStageThreads>(lkt, kt_base, a.t.k_st, j0, T, a.t.dim, tid);
-    if constexpr (GRAD)
-      stage_rows_transposed<BN, DPS, TRS, kStageThreads>(lkst, ks_base, a.s.k_st, j0, T, a.s.dim, tid);
     if (tid < BN) {
       const int j = j0 + tid;
       lcol[tid] = (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
@@ -156,37 +136,6 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
     l_s = l_s * c_s + sum_s;
     l_t = l_t * c_t + sum_t;
     a_t = a_t * c_t + sum_a;
-
-    if constexpr (GRAD) {
-      // Rescale the accumulators only when some row's running max moved.
-      const bool moved = (c_s != 1.f) || (c_t != 1.f);
-      if (__any(moved)) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          u_s[db] *= c_s;
-          u_t[db] *= c_t;
-        }
-      }
-      u16 bs[16], bt[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        bs[r] = to_bits(ps[r], BF);  // the K_s products run in the student dtype
-        bt[r] = to_bits(pt[r], BF);
-      }
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const u16x8 bop_s = {bs[8 * m + 0], bs[8 * m + 1], bs[8 * m + 2], bs[8 * m + 3],
-                             bs[8 * m + 4], bs[8 * m + 5], bs[8 * m + 6], bs[8 * m + 7]};
-        const u16x8 bop_t = {bt[8 * m + 0], bt[8 * m + 1], bt[8 * m + 2], bt[8 * m + 3],
-                             bt[8 * m + 4], bt[8 * m + 5], bt[8 * m + 6], bt[8 * m + 7]};
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const u16x8 aop = load_tr_slots(lkst + (32 * db + l32) * TRS, m, half);
-          u_s[db] = mfma32<BF>(aop, bop_s, u_s[db]);
-          u_t[db] = mfma32<BF>(aop, bop_t, u_t[db]);
-        }
-      }
-    }
   }
 
   const bool ok = row_valid && l_s > 0.f && l_t > 0.f;
@@ -201,33 +150,11 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
     // exact for close maxima and the log ratio keeps its relative precision.
     f.row_out[row_index] = ok ? a_t / l_t + (m_s - m_t) + (fast_log2(l_s) - fast_log2(l_t)) * kLn2 : 0.f;
   }
-  if constexpr (GRAD) {
-    if (in_range) {
-      const float is = ok ? a.s.scale / l_s : 0.f;
-      const float it = ok ? a.s.scale / l_t : 0.f;
-      float* out = f.dq_out + row_index * a.s.dim;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = 32 * db + 8 * g + 4 * half;
-          if (d0 < a.s.dim) {
-            f32x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)  // both products rounded: identical rows give exactly 0
-              v[e] = mul_rn(u_s[db][4 * g + e], is) - mul_rn(u_t[db][4 * g + e], it);
-            *reinterpret_cast<f32x4*>(out + d0) = v;
-          }
-        }
-      }
-    }
-  }
 }
 
-// Fused path coverage: Ds == Dt and one dtype for both relations (other
-// shapes use the stage kernels); the in-pass gradient needs D <= 128.
+// Coverage: Ds == Dt and one dtype for both relations (other shapes run the
+// stage kernels).
 bool fused_fwd_supported(int ds, int dt, bool same_dtype);
-bool fused_fwd_grad_supported(int d);
-hipError_t launch_fused_fwd(const FusedArgs& f, int dp, bool bf16, bool grad, hipStream_t stream);
+hipError_t launch_fused_fwd(const FusedArgs& f, int dp, bool bf16, hipStream_t stream);
 
 }  // namespace lard

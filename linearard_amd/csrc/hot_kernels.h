@@ -1,0 +1,626 @@
+// Throughput kernels of the autograd path for Ds == Dt <= 128 and one dtype
+// (every shape train.py produces: Llama/Mistral heads are d=128 bf16).
+//
+//   transpose_keys_kernel  x [B,H,T,D] -> xT [B*H][D][Tp] (Tp = T rounded up to
+//                          64, zero padded), keys permuted inside each group of
+//                          16 by sigma = (0-3, 8-11, 4-7, 12-15).  With that
+//                          order the 8 keys a lane needs as the k-slots of the
+//                          second GEMM (accumulator rows 8*(r/4)+4*half+r%4)
+//                          are 16 contiguous bytes, one ds_read_b128.
+//   hot_fwd_kernel         forward of AttnKLAlignFn (integration.py:8-45):
+//                          per query row both online softmaxes (stage A for
+//                          student and teacher) and the KL (stage B), one pass.
+//   hot_dq_kernel          backward, row side (kernel_C.py:224-239): per query
+//                          row dq = sm_scale_s D K_s, D = P_s - P_t from the
+//                          forward's LSEs, cast to the input dtype before the
+//                          product exactly like kernel_C.py:232-233, so the
+//                          error is relative to D, not to P.
+//   hot_bwd_kernel         backward, column side (kernel_C.py:242-253): per key
+//                          column dk = sm_scale_s sum_i D_ij q_i, summed over
+//                          the GQA group by its owner (no atomics), plus the
+//                          row side when q is k, times dloss.
+//
+// Memory pipeline: K (fwd) / Q (bwd) tiles of 64 rows are copied HBM->LDS
+// with global_load_lds_dwordx4 (no staging registers) into one of two LDS
+// buffers while the other is consumed, one barrier per tile.  LDS tiles are
+// XOR-swizzled by 16-byte chunk so the MFMA operand reads (16 lanes at a
+// time, one row each) hit 16 distinct bank groups.
+#pragma once
+
+#include "fused_kernels.h"
+
+namespace lard {
+
+constexpr int kTile = 64;          // rows of K (fwd) or Q (bwd) per LDS tile
+constexpr int kFwdWaves = 8;       // forward: 8 x 32 query rows per workgroup
+constexpr int kDqWaves = 4;        // backward row side: 4 x 32 query rows per workgroup
+constexpr int kBwdWaves = 4;       // backward column side: 4 x 32 key columns per workgroup
+constexpr float kRescaleLog2 = 8.f;  // lazy max: rescale only when the max grows by > 2^8
+
+// 16 zero bytes: the source of every chunk outside the tensor (rows >= T,
+// columns >= D), so LDS tiles are exactly zero-padded without branches.
+static __device__ __attribute__((aligned(16))) const unsigned int g_zero16[4] = {0u, 0u, 0u, 0u};
+
+struct HotArgs {
+  RelArgs r;
+  const u16* xT;      // transposed student keys (dq) / queries (dk): [B*H][D][Tp]
+  int Tp;             // padded length of xT rows
+  float* lse_s_out;   // fwd: [B, Hq, T]
+  float* lse_t_out;
+  float* row_out;     // fwd: per-row KL
+  float* dq_out;      // dq kernel: [B, Hq, T, Ds]
+};
+
+__device__ __forceinline__ void lds_async16(const void* g, u16* lds_chunk0) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_chunk0, 16, 0, 0);
+}
+
+// Swizzled row tile [kTile][DP]: chunk c (8 elements) of row r is stored at
+// chunk index r*CPR + (c ^ (r & (CPR-1))).
+template <int DP>
+__device__ __forceinline__ const u16* row_chunk(const u16* tile, int r, int c) {
+  constexpr int CPR = DP / 8;
+  return tile + (r * CPR + (c ^ (r & (CPR - 1)))) * 8;
+}
+
+// Swizzled transposed tile [DP][kTile]: chunk c (8 keys) of row d at d*8 + (c ^ ((d>>1)&7)).
+__device__ __forceinline__ const u16* tr_chunk(const u16* tile, int d, int c) {
+  return tile + (d * 8 + (c ^ ((d >> 1) & 7))) * 8;
+}
+
+// Issue the async copy of rows [row0, row0 + kTile) x [0, DP) into a row tile.
+template <int DP, int NWAVES>
+__device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int64_t row_stride, int row0, int T, int dim,
+                                           int wave, int lane) {
+  constexpr int CPR = DP / 8;
+  constexpr int NINST = kTile * CPR / 64;
+#pragma unroll
+  for (int n = wave; n < NINST; n += NWAVES) {
+    const int p = 64 * n + lane;
+    const int r = p / CPR;
+    const int c = (p % CPR) ^ (r & (CPR - 1));
+    const int row = row0 + r;
+    const void* g = (row < T && c * 8 < dim) ? static_cast<const void*>(src + (int64_t)row * row_stride + c * 8)
+                                             : static_cast<const void*>(g_zero16);
+    lds_async16(g, tile + 64 * n * 8);
+  }
+}
+
+// Issue the async copy of the transposed tile [DP][kTile] starting at key0.
+template <int DP, int NWAVES>
+__device__ __forceinline__ void issue_tr(u16* tile, const u16* srcT, int Tp, int key0, int dim, int wave, int lane) {
+  constexpr int NINST = DP * 8 / 64;
+#pragma unroll
+  for (int n = wave; n < NINST; n += NWAVES) {
+    const int p = 64 * n + lane;
+    const int d = p >> 3;
+    const int c = (p & 7) ^ ((d >> 1) & 7);
+    const void* g = (d < dim) ? static_cast<const void*>(srcT + (int64_t)d * Tp + key0 + c * 8)
+                              : static_cast<const void*>(g_zero16);
+    lds_async16(g, tile + 64 * n * 8);
+  }
+}
+
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+__device__ __forceinline__ u16x8 pack8(const u16* v) { return (u16x8){v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]}; }
+
+// ----------------------------------------------------------------------------
+// forward: both online softmaxes and the KL, one pass (2 GEMMs per pair)
+// ----------------------------------------------------------------------------
+template <int DP, bool BF>
+__global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f) {
+  const RelArgs& a = f.r;
+  constexpr int KS = DP / 16;
+  constexpr int ROWS = kFwdWaves * 32;
+  __shared__ __attribute__((aligned(16))) u16 lks[2][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[2][kTile * DP];
+  __shared__ int lcolok[2][kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int T = a.T;
+  const int nrb = (T + ROWS - 1) / ROWS;
+  const int rb = nrb - 1 - (int)blockIdx.x;  // longest causal rows first
+  const int bh = blockIdx.y;
+  const int b = bh / a.Hq;
+  const int h = bh - b * a.Hq;
+  const int row0 = rb * ROWS;
+  const int my_i = row0 + w * 32 + l32;
+  const bool in_range = my_i < T;
+  const bool row_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_i);
+  const int causal = a.causal;
+  const int diag_sb = (row0 >> 5) + w;  // this wave's diagonal 32-key sub-block
+
+  u16x8 fq_s[KS], fq_t[KS];
+  {
+    const u16* ps = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh + (int64_t)my_i * a.s.q_st;
+    const u16* pt = a.t.q + (int64_t)b * a.t.q_sb + (int64_t)h * a.t.q_sh + (int64_t)my_i * a.t.q_st;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const int d0 = 16 * kk + 8 * half;
+      const bool ld = in_range && d0 < a.s.dim;
+      fq_s[kk] = ld ? *reinterpret_cast<const u16x8*>(ps + d0) : (u16x8)(0);
+      fq_t[kk] = ld ? *reinterpret_cast<const u16x8*>(pt + d0) : (u16x8)(0);
+    }
+  }
+
+  const float c2s = a.s.scale2, c2t = a.t.scale2;  // raw logit -> log2 units
+  const float ratio = a.t.scale / a.s.scale;      // x_t - x_s = scale_s * (ratio*st - ss)
+  const float thr_s = kRescaleLog2 / c2s, thr_t = kRescaleLog2 / c2t;
+  // Raw-unit reference maxima; a finite start makes the first valid block
+  // rescale the (zero) sums by exp2(-huge) = 0 without inf - inf.
+  float m_s = -1e30f, m_t = -1e30f;
+  float nm_s = 0.f, nm_t = 0.f;           // -m * c2, refreshed with m
+  float l_s = 0.f, l_t = 0.f, acc = 0.f;  // per-lane partial sums (half of the row's keys)
+
+  const int hs = h / a.s.group, ht = h / a.t.group;
+  const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
+  const u16* kt_base = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh;
+
+  const int nkt_all = (T + kTile - 1) / kTile;
+  const int ntiles = causal ? min(nkt_all, (row0 + ROWS - 1) / kTile + 1) : nkt_all;
+  // causal: the diagonal tiles first, so the running max is set by the
+  // dominant self-similarity and rescales are rare
+  auto tile_of = [&](int it) { return causal ? ntiles - 1 - it : it; };
+  auto issue_tile = [&](int it, int buf) {
+    const int j0 = tile_of(it) * kTile;
+    issue_rows<DP, kFwdWaves>(lks[buf], ks_base, a.s.k_st, j0, T, a.s.dim, w, lane);
+    issue_rows<DP, kFwdWaves>(lkt[buf], kt_base, a.t.k_st, j0, T, a.t.dim, w, lane);
+  };
+  auto col_ok = [&](int it) -> int {  // validity of key tid of tile it (threads < kTile)
+    const int j = tile_of(it) * kTile + tid;
+    return (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
+  };
+
+  issue_tile(0, 0);
+  int next_ok = tid < kTile ? col_ok(0) : 1;
+  wait_all_memory();
+  if (tid < kTile) lcolok[0][tid] = next_ok;
+  int tile_masked = __syncthreads_or(!next_ok);
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int kt0 = tile_of(it) * kTile;
+    if (it + 1 < ntiles) {
+      issue_tile(it + 1, buf ^ 1);
+      next_ok = tid < kTile ? col_ok(it + 1) : 1;
+    } else {
+      next_ok = 1;
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
+      if (causal && gsb > diag_sb) continue;
+      const bool masked = tile_masked || (causal && gsb == diag_sb);
+
+      f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int c = 2 * kk + half;
+        ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lks[buf], 32 * sb + l32, c)), fq_s[kk], ss);
+        st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lkt[buf], 32 * sb + l32, c)), fq_t[kk], st);
+      }
+      if (masked) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int jj = 32 * sb + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool v = lcolok[buf][jj] && (!causal || kt0 + jj <= my_i);
+          ss[r] = v ? ss[r] : kNegInf;
+          st[r] = v ? st[r] : kNegInf;
+        }
+      }
+      float mb_s = ss[0], mb_t = st[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) {
+        mb_s = fmaxf(mb_s, ss[r]);
+        mb_t = fmaxf(mb_t, st[r]);
+      }
+      mb_s = fmaxf(mb_s, xor32(mb_s));
+      mb_t = fmaxf(mb_t, xor32(mb_t));
+      const bool need_s = mb_s > m_s + thr_s;
+      const bool need_t = mb_t > m_t + thr_t;
+      if (__any(need_s || need_t)) {
+        const float ns = need_s ? mb_s : m_s;
+        const float nt = need_t ? mb_t : m_t;
+        const float cs = fast_exp2((m_s - ns) * c2s);
+        const float ct = fast_exp2((m_t - nt) * c2t);
+        m_s = ns;
+        m_t = nt;
+        nm_s = -m_s * c2s;
+        nm_t = -m_t * c2t;
+        l_s *= cs;
+        l_t *= ct;
+        acc *= ct;
+      }
+      if (masked) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p_t = fast_exp2(fmaf(st[r], c2t, nm_t));
+          l_s += fast_exp2(fmaf(ss[r], c2s, nm_s));
+          l_t += p_t;
+          acc += (st[r] == kNegInf) ? 0.f : p_t * fmaf(st[r], ratio, -ss[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p_t = fast_exp2(fmaf(st[r], c2t, nm_t));
+          l_s += fast_exp2(fmaf(ss[r], c2s, nm_s));
+          l_t += p_t;
+          acc = fmaf(p_t, fmaf(st[r], ratio, -ss[r]), acc);
+        }
+      }
+    }
+    wait_all_memory();
+    if (it + 1 < ntiles && tid < kTile) lcolok[buf ^ 1][tid] = next_ok;
+    tile_masked = __syncthreads_or(!next_ok);
+  }
+
+  l_s += xor32(l_s);
+  l_t += xor32(l_t);
+  acc += xor32(acc);
+  const bool ok = row_valid && l_s > 0.f && l_t > 0.f;
+  const float ms_nat = m_s * a.s.scale, mt_nat = m_t * a.t.scale;
+  const float lg_s = fast_log2(l_s), lg_t = fast_log2(l_t);
+  const int64_t row_index = (int64_t)bh * T + my_i;
+  if (in_range && half == 0) {
+    f.lse_s_out[row_index] = row_valid ? (l_s > 0.f ? fmaf(lg_s, kLn2, ms_nat) : kNegInf) : 0.f;
+    f.lse_t_out[row_index] = row_valid ? (l_t > 0.f ? fmaf(lg_t, kLn2, mt_nat) : kNegInf) : 0.f;
+    // KL = E_pt[x_t - x_s] + (m_s - m_t) + ln(l_s / l_t)  (natural units); no
+    // two rounded LSEs are subtracted
+    f.row_out[row_index] = ok ? acc * a.s.scale / l_t + (ms_nat - mt_nat) + (lg_s - lg_t) * kLn2 : 0.f;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// backward, row side: dq = sm_scale_s D K_s, one owner per query row
+// ----------------------------------------------------------------------------
+template <int DP, bool BF>
+__global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) {
+  const RelArgs& a = f.r;
+  constexpr int NT = kDqWaves * 64;
+  constexpr int KS = DP / 16;
+  constexpr int TRR = DP < 32 ? 32 : DP;  // transposed tile rows (>= one 32-wide d block)
+  constexpr int NDB = TRR / 32;
+  constexpr int ROWS = kDqWaves * 32;
+  __shared__ __attribute__((aligned(16))) u16 lks[2][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[2][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkst[2][TRR * kTile];
+  __shared__ int lcolok[2][kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int T = a.T;
+  const int nrb = (T + ROWS - 1) / ROWS;
+  const int rb = nrb - 1 - (int)blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.Hq;
+  const int h = bh - b * a.Hq;
+  const int row0 = rb * ROWS;
+  const int my_i = row0 + w * 32 + l32;
+  const bool in_range = my_i < T;
+  const int causal = a.causal;
+  const int diag_sb = (row0 >> 5) + w;
+
+  if constexpr (DP < 32) {  // rows DP..31 of the transposed tiles stay zero
+    for (int c = tid; c < 2 * TRR * kTile; c += NT) {
+      const int buf = c / (TRR * kTile), e = c % (TRR * kTile);
+      if (e >= DP * kTile) lkst[buf][e] = 0;
+    }
+  }
+
+  u16x8 fq_s[KS], fq_t[KS];
+  {
+    const u16* ps = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh + (int64_t)my_i * a.s.q_st;
+    const u16* pt = a.t.q + (int64_t)b * a.t.q_sb + (int64_t)h * a.t.q_sh + (int64_t)my_i * a.t.q_st;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const int d0 = 16 * kk + 8 * half;
+      const bool ld = in_range && d0 < a.s.dim;
+      fq_s[kk] = ld ? *reinterpret_cast<const u16x8*>(ps + d0) : (u16x8)(0);
+      fq_t[kk] = ld ? *reinterpret_cast<const u16x8*>(pt + d0) : (u16x8)(0);
+    }
+  }
+  // Row normalisers in log2 units; rows outside the valid set get +inf, so
+  // exp2(x - inf) = 0 removes them (kernel_C.py:155-161, :256).
+  float nls2, nlt2;
+  bool ok;
+  {
+    float ls = 0.f, lt = 0.f;
+    bool rv = false;
+    if (in_range) {
+      rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_i);
+      ls = a.lse_s_in[(int64_t)bh * T + my_i];
+      lt = a.lse_t_in[(int64_t)bh * T + my_i];
+    }
+    ok = rv && ls != kNegInf && lt != kNegInf;
+    nls2 = ok ? -ls * kLog2e : kNegInf;
+    nlt2 = ok ? -lt * kLog2e : kNegInf;
+  }
+  const float c2s = a.s.scale2, c2t = a.t.scale2;
+  f32x16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dq[db] = (f32x16)(0.f);
+
+  const int hs = h / a.s.group, ht = h / a.t.group;
+  const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
+  const u16* kt_base = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh;
+  const u16* kst_base = f.xT + ((int64_t)b * a.s.hkv + hs) * a.s.dim * (int64_t)f.Tp;
+
+  const int nkt_all = (T + kTile - 1) / kTile;
+  const int ntiles = causal ? min(nkt_all, (row0 + ROWS - 1) / kTile + 1) : nkt_all;
+  auto issue_tile = [&](int t, int buf) {
+    const int j0 = t * kTile;
+    issue_rows<DP, kDqWaves>(lks[buf], ks_base, a.s.k_st, j0, T, a.s.dim, w, lane);
+    issue_rows<DP, kDqWaves>(lkt[buf], kt_base, a.t.k_st, j0, T, a.t.dim, w, lane);
+    issue_tr<DP, kDqWaves>(lkst[buf], kst_base, f.Tp, j0, a.s.dim, w, lane);
+  };
+  auto col_ok = [&](int t) -> int {
+    const int j = t * kTile + tid;
+    return (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
+  };
+
+  issue_tile(0, 0);
+  int next_ok = tid < kTile ? col_ok(0) : 1;
+  wait_all_memory();
+  if (tid < kTile) lcolok[0][tid] = next_ok;
+  int tile_masked = __syncthreads_or(!next_ok);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) {
+      issue_tile(t + 1, buf ^ 1);
+      next_ok = tid < kTile ? col_ok(t + 1) : 1;
+    } else {
+      next_ok = 1;
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int gsb = 2 * t + sb;
+      if (causal && gsb > diag_sb) continue;
+      const bool masked = tile_masked || (causal && gsb == diag_sb);
+      f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int c = 2 * kk + half;
+        ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lks[buf], 32 * sb + l32, c)), fq_s[kk], ss);
+        st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lkt[buf], 32 * sb + l32, c)), fq_t[kk], st);
+      }
+      u16 dv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float dd = fast_exp2(fmaf(ss[r], c2s, nls2)) - fast_exp2(fmaf(st[r], c2t, nlt2));
+        if (masked) {
+          const int jj = 32 * sb + 8 * (r >> 2) + 4 * half + (r & 3);
+          dd = (lcolok[buf][jj] && (!causal || t * kTile + jj <= my_i)) ? dd : 0.f;
+        }
+        dv[r] = to_bits(dd, BF);  // D cast to the input dtype (kernel_C.py:233)
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const u16x8 bop = pack8(dv + 8 * m);
+        const int c = 2 * (2 * sb + m) + half;  // 8-key chunk of the permuted tile
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          dq[db] = mfma32<BF>(*reinterpret_cast<const u16x8*>(tr_chunk(lkst[buf], 32 * db + l32, c)), bop, dq[db]);
+      }
+    }
+    wait_all_memory();
+    if (t + 1 < ntiles && tid < kTile) lcolok[buf ^ 1][tid] = next_ok;
+    tile_masked = __syncthreads_or(!next_ok);
+  }
+
+  if (in_range) {
+    const float fs = ok ? a.s.scale * (a.dscale != nullptr ? *a.dscale : 1.f) : 0.f;
+    float* out = f.dq_out + ((int64_t)bh * T + my_i) * a.s.dim;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * db + 8 * g + 4 * half;
+        if (d0 < a.s.dim) {
+          const f32x4 v = {dq[db][4 * g] * fs, dq[db][4 * g + 1] * fs, dq[db][4 * g + 2] * fs, dq[db][4 * g + 3] * fs};
+          *reinterpret_cast<f32x4*>(out + d0) = v;
+        }
+      }
+    }
+  }
+}
+// ----------------------------------------------------------------------------
+// backward
+// ----------------------------------------------------------------------------
+template <int DP, bool BF>
+__global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArgs f) {
+  const RelArgs& a = f.r;
+  constexpr int NT = kBwdWaves * 64;
+  constexpr int KS = DP / 16;
+  constexpr int TRR = DP < 32 ? 32 : DP;
+  constexpr int NDB = TRR / 32;
+  constexpr int COLS = kBwdWaves * 32;
+  __shared__ __attribute__((aligned(16))) u16 lqs[2][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lqt[2][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lqst[2][TRR * kTile];
+  __shared__ __attribute__((aligned(16))) float llse_s[2][kTile];  // log2 units, +inf = row excluded
+  __shared__ __attribute__((aligned(16))) float llse_t[2][kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int T = a.T;
+  const int cb = blockIdx.x;  // small cb = longest causal columns, launched first
+  const int bg = blockIdx.y;
+  const int b = bg / a.s.hkv;
+  const int g = bg - b * a.s.hkv;
+  const int j0w = cb * COLS + w * 32;
+  const int my_j = j0w + l32;
+  const bool in_range = my_j < T;
+  const bool col_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_j);
+  const int causal = a.causal;
+  const int diag_sb = j0w >> 5;  // the 32-row sub-block holding this wave's diagonal
+
+  if constexpr (DP < 32) {
+    for (int c = tid; c < 2 * TRR * kTile; c += NT) {
+      const int buf = c / (TRR * kTile), e = c % (TRR * kTile);
+      if (e >= DP * kTile) lqst[buf][e] = 0;
+    }
+  }
+
+  u16x8 fk_s[KS], fk_t[KS];
+  {
+    const u16* p = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)g * a.s.k_sh + (int64_t)my_j * a.s.k_st;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const int d0 = 16 * kk + 8 * half;
+      fk_s[kk] = (in_range && d0 < a.s.dim) ? *reinterpret_cast<const u16x8*>(p + d0) : (u16x8)(0);
+    }
+  }
+  f32x16 dk[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dk[db] = (f32x16)(0.f);
+
+  const float c2s = a.s.scale2, c2t = a.t.scale2;
+  const int ntile_all = (T + kTile - 1) / kTile;
+  const int it0 = causal ? (cb * COLS) / kTile : 0;
+  int loaded_ht = -1;
+
+  for (int hh = 0; hh < a.s.group; ++hh) {
+    const int h = g * a.s.group + hh;
+    const int ht = h / a.t.group;
+    if (ht != loaded_ht) {
+      const u16* p = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh + (int64_t)my_j * a.t.k_st;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int d0 = 16 * kk + 8 * half;
+        fk_t[kk] = (in_range && d0 < a.t.dim) ? *reinterpret_cast<const u16x8*>(p + d0) : (u16x8)(0);
+      }
+      loaded_ht = ht;
+    }
+    const int64_t bh = (int64_t)b * a.Hq + h;
+    const u16* qs_base = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh;
+    const u16* qt_base = a.t.q + (int64_t)b * a.t.q_sb + (int64_t)h * a.t.q_sh;
+    const u16* qst_base = f.xT + bh * a.s.dim * (int64_t)f.Tp;
+
+    auto issue_tile = [&](int t, int buf) {
+      const int i0 = t * kTile;
+      issue_rows<DP, kBwdWaves>(lqs[buf], qs_base, a.s.q_st, i0, T, a.s.dim, w, lane);
+      issue_rows<DP, kBwdWaves>(lqt[buf], qt_base, a.t.q_st, i0, T, a.t.dim, w, lane);
+      issue_tr<DP, kBwdWaves>(lqst[buf], qst_base, f.Tp, i0, a.s.dim, w, lane);
+    };
+    // Row data: log2-domain LSE, +inf for rows outside the valid set so that
+    // exp2(x - inf) = 0 removes them without per-element tests.
+    auto row_data = [&](int t, float& o_s, float& o_t) {
+      const int i = t * kTile + tid;
+      float ls = 0.f, lt = 0.f;
+      bool rv = false;
+      if (i < T) {
+        rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + i);
+        ls = a.lse_s_in[bh * T + i];
+        lt = a.lse_t_in[bh * T + i];
+      }
+      const bool ok = rv && ls != kNegInf && lt != kNegInf;
+      o_s = ok ? ls * kLog2e : __builtin_inff();
+      o_t = ok ? lt * kLog2e : __builtin_inff();
+    };
+
+    float nls = 0.f, nlt = 0.f;
+    issue_tile(it0, 0);
+    if (tid < kTile) row_data(it0, nls, nlt);
+    wait_all_memory();
+    if (tid < kTile) {
+      llse_s[0][tid] = nls;
+      llse_t[0][tid] = nlt;
+    }
+    __syncthreads();
+
+    for (int t = it0; t < ntile_all; ++t) {
+      const int buf = (t - it0) & 1;
+      if (t + 1 < ntile_all) {
+        issue_tile(t + 1, buf ^ 1);
+        if (tid < kTile) row_data(t + 1, nls, nlt);
+      }
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int gsb = 2 * t + sb;
+        if (causal && gsb < diag_sb) continue;
+        const bool diag = causal && gsb == diag_sb;
+        f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          const int c = 2 * kk + half;
+          ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lqs[buf], 32 * sb + l32, c)), fk_s[kk], ss);
+          st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lqt[buf], 32 * sb + l32, c)), fk_t[kk], st);
+        }
+        u16 dv[16];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int ii0 = 32 * sb + 8 * r4 + 4 * half;
+          const f32x4 ls4 = *reinterpret_cast<const f32x4*>(&llse_s[buf][ii0]);
+          const f32x4 lt4 = *reinterpret_cast<const f32x4*>(&llse_t[buf][ii0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            float dd = fast_exp2(fmaf(ss[r], c2s, -ls4[e])) - fast_exp2(fmaf(st[r], c2t, -lt4[e]));
+            if (diag) dd = (t * kTile + ii0 + e >= my_j) ? dd : 0.f;
+            dv[r] = to_bits(dd, BF);  // D cast to the input dtype (kernel_C.py:233)
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const u16x8 bop = pack8(dv + 8 * m);
+          const int c = 2 * (2 * sb + m) + half;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+            dk[db] = mfma32<BF>(*reinterpret_cast<const u16x8*>(tr_chunk(lqst[buf], 32 * db + l32, c)), bop, dk[db]);
+        }
+      }
+      wait_all_memory();
+      if (t + 1 < ntile_all && tid < kTile) {
+        llse_s[buf ^ 1][tid] = nls;
+        llse_t[buf ^ 1][tid] = nlt;
+      }
+      __syncthreads();
+    }
+  }
+
+  if (in_range) {
+    const int64_t off = ((int64_t)bg * T + my_j) * a.s.dim;
+    float* out = a.dk_out + off;
+    const float fs = a.s.scale;
+    const float mult = a.dscale != nullptr ? *a.dscale : 1.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d0 = 32 * db + 8 * gq + 4 * half;
+        if (d0 < a.s.dim) {
+          f32x4 v = {dk[db][4 * gq] * fs, dk[db][4 * gq + 1] * fs, dk[db][4 * gq + 2] * fs, dk[db][4 * gq + 3] * fs};
+          if (!col_valid) v = (f32x4)(0.f);  // masked key columns get no gradient (kernel_C.py:252-253)
+          if (a.dk_add != nullptr) v += *reinterpret_cast<const f32x4*>(a.dk_add + off + d0);
+          if (a.dscale != nullptr) v *= mult;
+          *reinterpret_cast<f32x4*>(out + d0) = v;
+        }
+      }
+    }
+  }
+}
+
+// Transposed, key-permuted copy of x for the second GEMM of both kernels.
+__global__ void transpose_keys_kernel(const u16* __restrict__ x, int64_t sb, int64_t sh, int64_t st, int H, int T,
+                                      int D, int Tp, u16* __restrict__ xT);
+
+bool hot_supported(int ds, int dt, bool same_dtype);
+hipError_t launch_transpose_keys(const u16* x, int64_t sb, int64_t sh, int64_t st, int B, int H, int T, int D, int Tp,
+                                 u16* xT, hipStream_t stream);
+hipError_t launch_hot_fwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
+hipError_t launch_hot_dq(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
+hipError_t launch_hot_bwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
+
+}  // namespace lard

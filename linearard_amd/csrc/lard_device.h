@@ -65,19 +65,19 @@ struct RelArgs {
   float* row_out;     // [B, Hq, T] per-row KL (mode KL)
   float* dq_out;      // [B, Hq, T, Ds] fp32 (mode DQ)
   float* dk_out;      // [B, Hkv_s, T, Ds] fp32 (dk kernel)
-  // Optional epilogue of the dk kernel used by the autograd backward:
+  // Optional epilogues used by the autograd backward:
+  //   dq_out = scale_s * dq * (*dscale)
   //   dk_out = (scale_s * dk + dk_add) * (*dscale)
   const float* dk_add;  // [B, Hkv_s, T, Ds] or null (self relation: the row-side term dq)
   const float* dscale;  // device scalar or null (autograd's dloss)
 };
 
-// Outputs of the fused forward (one pass: both LSEs, per-row KL, row-side grad).
+// Outputs of the fused forward (one pass: both LSEs and the per-row KL).
 struct FusedArgs {
   RelArgs r;
   float* lse_s_out;   // [B, Hq, T]
   float* lse_t_out;   // [B, Hq, T]
   float* row_out;     // [B, Hq, T] per-row KL
-  float* dq_out;      // [B, Hq, T, Ds] sm_scale_s (P_s - P_t) K_s, or null
 };
 
 __device__ __forceinline__ bool mask_at(const void* m, int kind, int64_t idx) {

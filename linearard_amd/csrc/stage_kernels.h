@@ -221,7 +221,8 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
     const float v = ok ? kl_acc : 0.f;  // kernel_B.py:216
     if (in_range && half == 0) a.row_out[row_index] = v;
   } else {
-    const float f = ok ? a.s.scale : 0.f;  // alpha_s, invalid rows zeroed (kernel_C.py:256)
+    // alpha_s (times dloss when asked), invalid rows zeroed (kernel_C.py:256)
+    const float f = ok ? a.s.scale * (a.dscale != nullptr ? *a.dscale : 1.f) : 0.f;
     if (in_range) {
       float* out = a.dq_out + row_index * a.s.dim;
 #pragma unroll
