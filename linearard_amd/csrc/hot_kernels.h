@@ -33,8 +33,8 @@ namespace lard {
 
 constexpr int kTile = 64;          // rows of K (fwd) or Q (bwd) per LDS tile
 constexpr int kFwdWaves = 8;       // forward: 8 x 32 query rows per workgroup
-constexpr int kDqWaves = 4;        // backward row side: 4 x 32 query rows per workgroup
-constexpr int kBwdWaves = 4;       // backward column side: 4 x 32 key columns per workgroup
+constexpr int kDqWaves = 8;        // backward row side: 8 x 32 query rows per workgroup
+constexpr int kBwdWaves = 8;       // backward column side: 8 x 32 key columns per workgroup
 constexpr float kRescaleLog2 = 8.f;  // lazy max: rescale only when the max grows by > 2^8
 
 // 16 zero bytes: the source of every chunk outside the tensor (rows >= T,
