@@ -5,10 +5,12 @@
 // returns, plus the alignment rules of the 16-byte vector loads.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 
 #include "../../include/linearard_amd.h"
@@ -148,6 +150,101 @@ int check_two_sided(const lard_tensor4* qs, const lard_tensor4* ks, const float*
   return check_grid(qs->size[0] * (qs->size[1] > ks->size[1] ? qs->size[1] : ks->size[1]));
 }
 
+// The throughput kernels run one flat grid of (T / 256) x B x heads workgroups.
+int check_blocks(int64_t B, int64_t heads, int64_t T) {
+  if ((T + lard::kRows - 1) / lard::kRows * B * heads > (int64_t)INT32_MAX)
+    return fail(LARD_ERR_UNSUPPORTED, "B * heads * T / %d must be < 2^31", lard::kRows);
+  return LARD_OK;
+}
+
+int64_t padded_len(int64_t T) { return (T + lard::kTile - 1) / lard::kTile * lard::kTile; }
+
+// The throughput kernels address one head of every operand with 32-bit byte
+// offsets: (T-1) * row_stride + D elements and the transposed D * Tp must
+// stay below 2^30 elements.  Larger heads run the stage kernels.
+bool hot_offsets_ok(std::initializer_list<const lard_tensor4*> ts, int64_t T) {
+  constexpr int64_t kMax = (int64_t)1 << 30;
+  for (const lard_tensor4* t : ts)
+    if ((T - 1) * t->stride[2] + t->size[3] >= kMax || t->size[3] * padded_len(T) >= kMax) return false;
+  return true;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Carves 256-byte aligned regions out of a caller workspace in a fixed
+// order; with a null base it only counts bytes (the *_workspace_bytes calls).
+class Carver {
+ public:
+  explicit Carver(void* base) : base_(static_cast<char*>(base)) {}
+  template <class T>
+  T* take(int64_t count) {
+    T* p = base_ != nullptr ? reinterpret_cast<T*>(base_ + off_) : nullptr;
+    off_ += align256((size_t)count * sizeof(T));
+    return p;
+  }
+  size_t bytes() const { return off_; }
+
+ private:
+  char* base_;
+  size_t off_ = 0;
+};
+
+// Loss reduction: per-row KL terms, then double partials.
+struct LossWs {
+  float* rows;
+  double* partial;
+};
+
+LossWs loss_layout(void* base, int64_t n, size_t* bytes) {
+  Carver c(base);
+  LossWs w;
+  w.rows = c.take<float>(n);
+  w.partial = c.take<double>(lard::kReduceBlocks);
+  if (bytes != nullptr) *bytes = c.bytes();
+  return w;
+}
+
+// Forward of the autograd path: loss regions + token validity.
+struct FwdWs {
+  LossWs loss;
+  unsigned char* tok_ok;
+};
+
+FwdWs fwd_layout(void* base, int64_t B, int64_t H, int64_t T, size_t* bytes) {
+  size_t loss_bytes = 0;
+  FwdWs w;
+  w.loss = loss_layout(base, B * H * T, &loss_bytes);
+  Carver c(base != nullptr ? static_cast<char*>(base) + loss_bytes : nullptr);
+  const int64_t Tp = padded_len(T);
+  w.tok_ok = c.take<unsigned char>(B * Tp);
+  if (bytes != nullptr) *bytes = loss_bytes + c.bytes();
+  return w;
+}
+
+// Backward of the autograd path: transposed keys (and queries unless q is k),
+// token validity, and the log2-domain row normalisers.
+struct BwdWs {
+  lard::u16* kT;
+  lard::u16* qT;
+  unsigned char* tok_ok;
+  float* nl_s;
+  float* nl_t;
+};
+
+BwdWs bwd_layout(void* base, int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, bool self_relation,
+                 size_t* bytes) {
+  Carver c(base);
+  BwdWs w;
+  const int64_t Tp = padded_len(T);
+  w.kT = c.take<lard::u16>(B * Hkv * D * Tp);
+  w.qT = self_relation ? w.kT : c.take<lard::u16>(B * Hq * D * Tp);
+  w.tok_ok = c.take<unsigned char>(B * Tp);
+  w.nl_s = c.take<float>(B * Hq * Tp);
+  w.nl_t = c.take<float>(B * Hq * Tp);
+  if (bytes != nullptr) *bytes = c.bytes();
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -177,7 +274,9 @@ int lard_lse_stats(const lard_tensor4* q, const lard_tensor4* k, const lard_mask
 
 size_t lard_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
-  return (size_t)(batch * heads * seq_len) * sizeof(float);
+  size_t bytes = 0;
+  loss_layout(nullptr, batch * heads * seq_len, &bytes);
+  return bytes;
 }
 
 int lard_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
@@ -199,13 +298,14 @@ int lard_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const float*
     fill_common(a, B, Hq, T, mask, causal);
     a.lse_s_in = lse_s;
     a.lse_t_in = lse_t;
-    a.row_out = static_cast<float*>(workspace);
+    const LossWs w = loss_layout(workspace, n, nullptr);
+    a.row_out = w.rows;
     if ((rc = hip_status(lard::launch_row_kl(a, padded_dim(qs->size[3]), padded_dim(qt->size[3]), st),
                          "kl_forward launch")) != LARD_OK)
       return rc;
+    return hip_status(lard::launch_reduce_sum(w.rows, n, w.partial, loss_out, st), "kl_forward reduce launch");
   }
-  return hip_status(lard::launch_reduce_sum(static_cast<const float*>(workspace), n, loss_out, st),
-                    "kl_forward reduce launch");
+  return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "kl_forward reduce launch");
 }
 
 int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
@@ -230,16 +330,11 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
   return hip_status(lard::launch_col_dk(a, dps, dpt, st), "kl_backward dk launch");
 }
 
-static int64_t padded_len(int64_t T) { return (T + lard::kTile - 1) / lard::kTile * lard::kTile; }
-
-static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
-
-static size_t transposed_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
-  return align256((size_t)(batch * heads * head_dim * padded_len(seq_len)) * sizeof(uint16_t));
-}
-
 size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
-  return lard_kl_forward_workspace_bytes(batch, heads, seq_len);
+  if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  size_t bytes = 0;
+  fwd_layout(nullptr, batch, heads, seq_len, &bytes);
+  return bytes;
 }
 
 int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
@@ -268,15 +363,23 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
     const int ds = (int)qs->size[3], dt = (int)qt->size[3];
     const bool same = qs->dtype == qt->dtype;
     const bool bf = qs->dtype == LARD_DTYPE_BF16;
-    if (lard::hot_supported(ds, dt, same) || lard::fused_fwd_supported(ds, dt, same)) {
+    const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
+    const bool hot = lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T);
+    if (hot || lard::fused_fwd_supported(ds, dt, same)) {
       lard::HotArgs f{};
       fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
       fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
       fill_common(f.r, B, Hq, T, mask, causal);
       f.lse_s_out = lse_s_out;
       f.lse_t_out = lse_t_out;
-      f.row_out = static_cast<float*>(workspace);
-      if (lard::hot_supported(ds, dt, same)) {
+      f.row_out = w.loss.rows;
+      if (hot) {
+        if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
+        f.Tp = (int)padded_len(T);
+        f.tok_ok = w.tok_ok;
+        if ((rc = hip_status(lard::launch_token_prep(f.r, f.Tp, w.tok_ok, st),
+                             "attn_kl_forward token prep launch")) != LARD_OK)
+          return rc;
         rc = hip_status(lard::launch_hot_fwd(f, padded_dim(ds), bf, st), "attn_kl_forward launch");
       } else {
         lard::FusedArgs g{};
@@ -297,21 +400,23 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
       fill_common(a, B, Hq, T, mask, causal);
       a.lse_s_in = lse_s_out;
       a.lse_t_in = lse_t_out;
-      a.row_out = static_cast<float*>(workspace);
+      a.row_out = w.loss.rows;
       if ((rc = hip_status(lard::launch_row_kl(a, padded_dim(ds), padded_dim(dt), st), "attn_kl_forward kl launch")) !=
           LARD_OK)
         return rc;
     }
+    return hip_status(lard::launch_reduce_sum(w.loss.rows, n, w.loss.partial, loss_out, st),
+                      "attn_kl_forward reduce launch");
   }
-  return hip_status(lard::launch_reduce_sum(static_cast<const float*>(workspace), n, loss_out, st),
-                    "attn_kl_forward reduce launch");
+  return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "attn_kl_forward reduce launch");
 }
 
 size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,
                                              int64_t head_dim, int self_relation) {
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
-  const size_t kt = transposed_bytes(batch, kv_heads, seq_len, head_dim);
-  return self_relation ? kt : kt + transposed_bytes(batch, heads, seq_len, head_dim);
+  size_t bytes = 0;
+  bwd_layout(nullptr, batch, heads, kv_heads, seq_len, head_dim, self_relation != 0, &bytes);
+  return bytes;
 }
 
 int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
@@ -341,36 +446,43 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
   a.lse_t_in = lse_t;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int ds = (int)qs->size[3], dt = (int)qt->size[3];
-  if (lard::hot_supported(ds, dt, qs->dtype == qt->dtype)) {
+  if (lard::hot_supported(ds, dt, qs->dtype == qt->dtype) && hot_offsets_ok({qs, ks, qt, kt}, T)) {
     const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+    if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
     const int Tp = (int)padded_len(T);
-    lard::u16* kT = static_cast<lard::u16*>(workspace);
-    lard::u16* qT = self_relation ? kT
-                                  : reinterpret_cast<lard::u16*>(static_cast<char*>(workspace) +
-                                                                 transposed_bytes(B, ks->size[1], T, ds));
+    const BwdWs w = bwd_layout(workspace, B, Hq, ks->size[1], T, ds, self_relation != 0, nullptr);
     if ((rc = hip_status(lard::launch_transpose_keys(static_cast<const lard::u16*>(ks->data), ks->stride[0],
                                                      ks->stride[1], ks->stride[2], (int)B, (int)ks->size[1], (int)T,
-                                                     ds, Tp, kT, st),
+                                                     ds, Tp, w.kT, st),
                          "attn_kl_backward transpose launch")) != LARD_OK)
       return rc;
     if (!self_relation &&
         (rc = hip_status(lard::launch_transpose_keys(static_cast<const lard::u16*>(qs->data), qs->stride[0],
                                                      qs->stride[1], qs->stride[2], (int)B, (int)Hq, (int)T, ds, Tp,
-                                                     qT, st),
+                                                     w.qT, st),
                          "attn_kl_backward transpose launch")) != LARD_OK)
+      return rc;
+    if ((rc = hip_status(lard::launch_token_prep(a, Tp, w.tok_ok, st),
+                         "attn_kl_backward token prep launch")) != LARD_OK)
+      return rc;
+    if ((rc = hip_status(lard::launch_row_prep(a, Tp, w.tok_ok, w.nl_s, w.nl_t, st),
+                         "attn_kl_backward row prep launch")) != LARD_OK)
       return rc;
     lard::HotArgs f{};
     f.r = a;
     f.Tp = Tp;
-    f.xT = kT;
+    f.xT = w.kT;
+    f.tok_ok = w.tok_ok;
+    f.nl_s = w.nl_s;
+    f.nl_t = w.nl_t;
     f.dq_out = dq_dst;
     f.r.dscale = self_relation ? nullptr : dloss;
     if ((rc = hip_status(lard::launch_hot_dq(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, st),
                          "attn_kl_backward dq launch")) != LARD_OK)
       return rc;
-    f.xT = qT;
+    f.xT = w.qT;
     f.r.dk_out = dk_out;
     f.r.dk_add = self_relation ? dk_out : nullptr;
     f.r.dscale = dloss;

@@ -7,6 +7,10 @@
 //                          order the 8 keys a lane needs as the k-slots of the
 //                          second GEMM (accumulator rows 8*(r/4)+4*half+r%4)
 //                          are 16 contiguous bytes, one ds_read_b128.
+//   token_prep_kernel      per token: valid (j < T and mask != 0), one byte.
+//   row_prep_kernel        per query row of the backward: -lse * log2(e) for
+//                          student and teacher, -inf outside the valid set
+//                          (kernel_C.py:155-161), so exp2(x * c + nl) is P.
 //   hot_fwd_kernel         forward of AttnKLAlignFn (integration.py:8-45):
 //                          per query row both online softmaxes (stage A for
 //                          student and teacher) and the KL (stage B), one pass.
@@ -20,39 +24,84 @@
 //                          the GQA group by its owner (no atomics), plus the
 //                          row side when q is k, times dloss.
 //
-// Memory pipeline: K (fwd) / Q (bwd) tiles of 64 rows are copied HBM->LDS
-// with global_load_lds_dwordx4 (no staging registers) into one of two LDS
-// buffers while the other is consumed, one barrier per tile.  LDS tiles are
-// XOR-swizzled by 16-byte chunk so the MFMA operand reads (16 lanes at a
+// Memory pipeline: K (fwd, dq) / Q (dk) tiles of 64 rows are copied
+// HBM->LDS with global_load_lds_dwordx4 (no staging registers) into a ring
+// of three LDS buffers: tile t+2 is in flight while tile t is consumed, one
+// barrier per tile.  Every wave issues the same number of copies per tile,
+// so "all but the newest tile landed" is one s_waitcnt vmcnt(N).  LDS tiles
+// are XOR-swizzled by 16-byte chunk so the MFMA operand reads (16 lanes at a
 // time, one row each) hit 16 distinct bank groups.
+//
+// Work order: workgroups are numbered so that each XCD (8 per MI355X, one L2
+// each; workgroups are dealt to XCDs round robin) receives a contiguous range
+// of (head, tile) work, longest causal tiles first within each head.
 #pragma once
 
 #include "fused_kernels.h"
 
 namespace lard {
 
-constexpr int kTile = 64;          // rows of K (fwd) or Q (bwd) per LDS tile
-constexpr int kFwdWaves = 8;       // forward: 8 x 32 query rows per workgroup
-constexpr int kDqWaves = 8;        // backward row side: 8 x 32 query rows per workgroup
-constexpr int kBwdWaves = 8;       // backward column side: 8 x 32 key columns per workgroup
+constexpr int kTile = 64;     // rows of K (fwd, dq) or Q (dk) per LDS tile
+constexpr int kWaves = 8;     // waves per workgroup: 8 x 32 rows / columns
+constexpr int kRows = kWaves * 32;
+constexpr int kStages = 3;    // LDS ring depth
+constexpr int kXcds = 8;
 constexpr float kRescaleLog2 = 8.f;  // lazy max: rescale only when the max grows by > 2^8
-
-// 16 zero bytes: the source of every chunk outside the tensor (rows >= T,
-// columns >= D), so LDS tiles are exactly zero-padded without branches.
-static __device__ __attribute__((aligned(16))) const unsigned int g_zero16[4] = {0u, 0u, 0u, 0u};
 
 struct HotArgs {
   RelArgs r;
-  const u16* xT;      // transposed student keys (dq) / queries (dk): [B*H][D][Tp]
-  int Tp;             // padded length of xT rows
-  float* lse_s_out;   // fwd: [B, Hq, T]
+  const u16* xT;                 // transposed student keys (dq) / queries (dk): [B*H][D][Tp]
+  int Tp;                        // T rounded up to kTile
+  const unsigned char* tok_ok;   // [B][Tp] token validity
+  const float* nl_s;             // backward: [B*Hq][Tp] -lse_s*log2(e), -inf for excluded rows
+  const float* nl_t;
+  float* lse_s_out;              // fwd: [B, Hq, T]
   float* lse_t_out;
-  float* row_out;     // fwd: per-row KL
-  float* dq_out;      // dq kernel: [B, Hq, T, Ds]
+  float* row_out;                // fwd: per-row KL
+  float* dq_out;                 // dq: [B, Hq, T, Ds]
 };
 
-__device__ __forceinline__ void lds_async16(const void* g, u16* lds_chunk0) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_chunk0, 16, 0, 0);
+// 16 bytes per lane HBM -> LDS: lane l copies base + voff (bytes) to
+// lds_chunk0 + 16*l.  The base is uniform (an SGPR pair, the "saddr" form, so
+// each copy needs one VGPR offset), and so is the LDS destination (M0).
+// Issued as inline asm on purpose: the compiler cannot prove that later
+// ds_reads of OTHER ring buffers do not alias the copies in flight, and for
+// the builtin it inserts s_waitcnt vmcnt(0) before every LDS read, which
+// serialises the ring.  The kernels order the copies themselves with
+// wait_vmcnt<N>() + a barrier; the "memory" clobber keeps the compiler from
+// moving LDS accesses across the issue point.
+__device__ __forceinline__ void lds_async16(const void* base, unsigned voff, void* lds_chunk0) {
+  // readfirstlane is int -> int: both halves go back through unsigned so the
+  // low word is zero-extended (a sign-extended low word would corrupt the
+  // high word of the address).
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(b))));
+  const unsigned hi =
+      static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(b >> 32))));
+  const uint64_t sbase = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_chunk0);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// (expcnt / lgkmcnt fields left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+}
+
+// Position of workgroup `bid` in a work list of n items after the XCD-aware
+// renumbering: XCD x = bid % 8 gets the contiguous range starting at
+// x * (n / 8) + min(x, n % 8).
+__device__ __forceinline__ int xcd_item(int bid, int n) {
+  const int x = bid % kXcds, m = bid / kXcds;
+  const int base = n / kXcds, rem = n % kXcds;
+  return x * base + min(x, rem) + m;
 }
 
 // Swizzled row tile [kTile][DP]: chunk c (8 elements) of row r is stored at
@@ -68,40 +117,60 @@ __device__ __forceinline__ const u16* tr_chunk(const u16* tile, int d, int c) {
   return tile + (d * 8 + (c ^ ((d >> 1) & 7))) * 8;
 }
 
-// Issue the async copy of rows [row0, row0 + kTile) x [0, DP) into a row tile.
-template <int DP, int NWAVES>
-__device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int64_t row_stride, int row0, int T, int dim,
+// Copies per wave per tile.  They are uniform across waves when the chunk
+// count of a tile is a multiple of the wave count (D >= 64); otherwise the
+// kernels wait for everything (vmcnt 0) and lose only the look-ahead.
+template <int DP>
+struct TileCopies {
+  static constexpr int kRowInst = kTile * (DP / 8) / 64;  // per row tile
+  static constexpr int kTrInst = DP * 8 / 64;             // per transposed tile
+  static constexpr bool kUniform = kRowInst % kWaves == 0;
+  static constexpr int kRowPerWave = kRowInst / kWaves;
+  static constexpr int kTrPerWave = kTrInst / kWaves;
+};
+
+// Issue the async copy of rows [row0, row0 + kTile) x [0, DP) of one head
+// (src = its row 0, rows row_stride elements apart) into a row tile.  Rows
+// >= T and column chunks >= dim copy clamped, finite data instead of zeros:
+// every consumer zeroes or masks their contribution (key rows >= T are
+// invalid tokens, query rows >= T have -inf normalisers, padded columns meet
+// zero register operands).  The host keeps every offset below 2^31 bytes.
+template <int DP>
+__device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_stride, int row0, int T, int dim,
                                            int wave, int lane) {
   constexpr int CPR = DP / 8;
-  constexpr int NINST = kTile * CPR / 64;
+  constexpr int NINST = TileCopies<DP>::kRowInst;
 #pragma unroll
-  for (int n = wave; n < NINST; n += NWAVES) {
+  for (int n = wave; n < NINST; n += kWaves) {
     const int p = 64 * n + lane;
     const int r = p / CPR;
-    const int c = (p % CPR) ^ (r & (CPR - 1));
-    const int row = row0 + r;
-    const void* g = (row < T && c * 8 < dim) ? static_cast<const void*>(src + (int64_t)row * row_stride + c * 8)
-                                             : static_cast<const void*>(g_zero16);
-    lds_async16(g, tile + 64 * n * 8);
+    int c = (p % CPR) ^ (r & (CPR - 1));
+    c = c * 8 < dim ? c : 0;
+    const int row = min(row0 + r, T - 1);
+    lds_async16(src, (unsigned)(row * row_stride + c * 8) * 2u, tile + 64 * n * 8);
   }
 }
 
-// Issue the async copy of the transposed tile [DP][kTile] starting at key0.
-template <int DP, int NWAVES>
+// Issue the async copy of the transposed tile [DP][kTile] starting at key0
+// (srcT = one head of xT, rows Tp apart).  Rows d >= dim copy row 0: they
+// feed output columns that are never stored.
+template <int DP>
 __device__ __forceinline__ void issue_tr(u16* tile, const u16* srcT, int Tp, int key0, int dim, int wave, int lane) {
-  constexpr int NINST = DP * 8 / 64;
+  constexpr int NINST = TileCopies<DP>::kTrInst;
 #pragma unroll
-  for (int n = wave; n < NINST; n += NWAVES) {
+  for (int n = wave; n < NINST; n += kWaves) {
     const int p = 64 * n + lane;
     const int d = p >> 3;
     const int c = (p & 7) ^ ((d >> 1) & 7);
-    const void* g = (d < dim) ? static_cast<const void*>(srcT + (int64_t)d * Tp + key0 + c * 8)
-                              : static_cast<const void*>(g_zero16);
-    lds_async16(g, tile + 64 * n * 8);
+    const int dd = d < dim ? d : 0;
+    lds_async16(srcT, (unsigned)(dd * Tp + key0 + c * 8) * 2u, tile + 64 * n * 8);
   }
 }
 
-__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+// One copy per wave: 64 bytes (lanes 0-3, 16 each) of `src` into `slot`.
+__device__ __forceinline__ void issue_small(void* slot, const void* src, int lane) {
+  if (lane < 4) lds_async16(src, 16u * lane, slot);
+}
 
 __device__ __forceinline__ u16x8 pack8(const u16* v) { return (u16x8){v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]}; }
 
@@ -109,13 +178,14 @@ __device__ __forceinline__ u16x8 pack8(const u16* v) { return (u16x8){v[0], v[1]
 // forward: both online softmaxes and the KL, one pass (2 GEMMs per pair)
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
-__global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f) {
+__global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   const RelArgs& a = f.r;
+  using TC = TileCopies<DP>;
   constexpr int KS = DP / 16;
-  constexpr int ROWS = kFwdWaves * 32;
-  __shared__ __attribute__((aligned(16))) u16 lks[2][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[2][kTile * DP];
-  __shared__ int lcolok[2][kTile];
+  constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
+  __shared__ __attribute__((aligned(16))) u16 lks[kStages][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[kStages][kTile * DP];
+  __shared__ __attribute__((aligned(16))) unsigned char ltok[kStages][kWaves][kTile];  // one copy per wave
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -123,12 +193,13 @@ __global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int T = a.T;
-  const int nrb = (T + ROWS - 1) / ROWS;
-  const int rb = nrb - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int bh = blockIdx.y;
+  const int nrb = (T + kRows - 1) / kRows;
+  const int item = xcd_item(blockIdx.x, nrb * a.B * a.Hq);
+  const int bh = item / nrb;
+  const int rb = nrb - 1 - (item - bh * nrb);  // longest causal rows first
   const int b = bh / a.Hq;
   const int h = bh - b * a.Hq;
-  const int row0 = rb * ROWS;
+  const int row0 = rb * kRows;
   const int my_i = row0 + w * 32 + l32;
   const bool in_range = my_i < T;
   const bool row_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_i);
@@ -160,42 +231,47 @@ __global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f
   const int hs = h / a.s.group, ht = h / a.t.group;
   const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
   const u16* kt_base = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh;
+  const unsigned char* tok = f.tok_ok + (int64_t)b * f.Tp;
 
-  const int nkt_all = (T + kTile - 1) / kTile;
-  const int ntiles = causal ? min(nkt_all, (row0 + ROWS - 1) / kTile + 1) : nkt_all;
+  const int nkt_all = f.Tp / kTile;
+  const int ntiles = causal ? min(nkt_all, (row0 + kRows - 1) / kTile + 1) : nkt_all;
   // causal: the diagonal tiles first, so the running max is set by the
   // dominant self-similarity and rescales are rare
   auto tile_of = [&](int it) { return causal ? ntiles - 1 - it : it; };
-  auto issue_tile = [&](int it, int buf) {
+  auto issue_tile = [&](int it) {
+    const int buf = it % kStages;
     const int j0 = tile_of(it) * kTile;
-    issue_rows<DP, kFwdWaves>(lks[buf], ks_base, a.s.k_st, j0, T, a.s.dim, w, lane);
-    issue_rows<DP, kFwdWaves>(lkt[buf], kt_base, a.t.k_st, j0, T, a.t.dim, w, lane);
-  };
-  auto col_ok = [&](int it) -> int {  // validity of key tid of tile it (threads < kTile)
-    const int j = tile_of(it) * kTile + tid;
-    return (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
+    issue_rows<DP>(lks[buf], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+    issue_rows<DP>(lkt[buf], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    issue_small(ltok[buf][w], tok + j0, lane);
   };
 
-  issue_tile(0, 0);
-  int next_ok = tid < kTile ? col_ok(0) : 1;
-  wait_all_memory();
-  if (tid < kTile) lcolok[0][tid] = next_ok;
-  int tile_masked = __syncthreads_or(!next_ok);
+  // The register operands loaded above must have landed before the ring
+  // starts: the compiler does not count the asm copies, so a wait it placed
+  // for these loads inside the loop would be vmcnt(0) and drain the ring.
+  wait_vmcnt<0>();
+  issue_tile(0);
+  if (ntiles > 1) issue_tile(1);
+  if (TC::kUniform && ntiles > 1)
+    wait_vmcnt<kPerWave>();
+  else
+    wait_vmcnt<0>();
+  __syncthreads();
 
   for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
+    const int buf = it % kStages;
     const int kt0 = tile_of(it) * kTile;
-    if (it + 1 < ntiles) {
-      issue_tile(it + 1, buf ^ 1);
-      next_ok = tid < kTile ? col_ok(it + 1) : 1;
-    } else {
-      next_ok = 1;
-    }
+    const bool more = it + 2 < ntiles;
+    if (more) issue_tile(it + 2);
+    // Tiles with an invalid key take the masked path.  The test reads the
+    // wave's LDS copy of the validity bytes (a global read here would make
+    // the wave drain its copies in flight).
+    const bool col_masked = __any(ltok[buf][w][lane] == 0);
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
       if (causal && gsb > diag_sb) continue;
-      const bool masked = tile_masked || (causal && gsb == diag_sb);
+      const bool masked = col_masked || (causal && gsb == diag_sb);
 
       f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
 #pragma unroll
@@ -208,7 +284,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int jj = 32 * sb + 8 * (r >> 2) + 4 * half + (r & 3);
-          const bool v = lcolok[buf][jj] && (!causal || kt0 + jj <= my_i);
+          const bool v = ltok[buf][w][jj] && (!causal || kt0 + jj <= my_i);
           ss[r] = v ? ss[r] : kNegInf;
           st[r] = v ? st[r] : kNegInf;
         }
@@ -254,9 +330,11 @@ __global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f
         }
       }
     }
-    wait_all_memory();
-    if (it + 1 < ntiles && tid < kTile) lcolok[buf ^ 1][tid] = next_ok;
-    tile_masked = __syncthreads_or(!next_ok);
+    if (TC::kUniform && more)
+      wait_vmcnt<kPerWave>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
   }
 
   l_s += xor32(l_s);
@@ -279,17 +357,18 @@ __global__ __launch_bounds__(kFwdWaves * 64) void hot_fwd_kernel(const HotArgs f
 // backward, row side: dq = sm_scale_s D K_s, one owner per query row
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
-__global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) {
+__global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   const RelArgs& a = f.r;
-  constexpr int NT = kDqWaves * 64;
+  using TC = TileCopies<DP>;
+  constexpr int NT = kWaves * 64;
   constexpr int KS = DP / 16;
   constexpr int TRR = DP < 32 ? 32 : DP;  // transposed tile rows (>= one 32-wide d block)
   constexpr int NDB = TRR / 32;
-  constexpr int ROWS = kDqWaves * 32;
-  __shared__ __attribute__((aligned(16))) u16 lks[2][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[2][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkst[2][TRR * kTile];
-  __shared__ int lcolok[2][kTile];
+  constexpr int kPerWave = 2 * TC::kRowPerWave + TC::kTrPerWave + 1;
+  __shared__ __attribute__((aligned(16))) u16 lks[kStages][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[kStages][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkst[kStages][TRR * kTile];
+  __shared__ __attribute__((aligned(16))) unsigned char ltok[kStages][kWaves][kTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -297,19 +376,20 @@ __global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) 
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int T = a.T;
-  const int nrb = (T + ROWS - 1) / ROWS;
-  const int rb = nrb - 1 - (int)blockIdx.x;
-  const int bh = blockIdx.y;
+  const int nrb = (T + kRows - 1) / kRows;
+  const int item = xcd_item(blockIdx.x, nrb * a.B * a.Hq);
+  const int bh = item / nrb;
+  const int rb = nrb - 1 - (item - bh * nrb);
   const int b = bh / a.Hq;
   const int h = bh - b * a.Hq;
-  const int row0 = rb * ROWS;
+  const int row0 = rb * kRows;
   const int my_i = row0 + w * 32 + l32;
   const bool in_range = my_i < T;
   const int causal = a.causal;
   const int diag_sb = (row0 >> 5) + w;
 
   if constexpr (DP < 32) {  // rows DP..31 of the transposed tiles stay zero
-    for (int c = tid; c < 2 * TRR * kTile; c += NT) {
+    for (int c = tid; c < kStages * TRR * kTile; c += NT) {
       const int buf = c / (TRR * kTile), e = c % (TRR * kTile);
       if (e >= DP * kTile) lkst[buf][e] = 0;
     }
@@ -327,22 +407,10 @@ __global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) 
       fq_t[kk] = ld ? *reinterpret_cast<const u16x8*>(pt + d0) : (u16x8)(0);
     }
   }
-  // Row normalisers in log2 units; rows outside the valid set get +inf, so
-  // exp2(x - inf) = 0 removes them (kernel_C.py:155-161, :256).
-  float nls2, nlt2;
-  bool ok;
-  {
-    float ls = 0.f, lt = 0.f;
-    bool rv = false;
-    if (in_range) {
-      rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_i);
-      ls = a.lse_s_in[(int64_t)bh * T + my_i];
-      lt = a.lse_t_in[(int64_t)bh * T + my_i];
-    }
-    ok = rv && ls != kNegInf && lt != kNegInf;
-    nls2 = ok ? -ls * kLog2e : kNegInf;
-    nlt2 = ok ? -lt * kLog2e : kNegInf;
-  }
+  // Row normalisers in log2 units, -inf outside the valid set (exp2 -> 0).
+  const float nls2 = in_range ? f.nl_s[(int64_t)bh * f.Tp + my_i] : kNegInf;
+  const float nlt2 = in_range ? f.nl_t[(int64_t)bh * f.Tp + my_i] : kNegInf;
+  const bool ok = nls2 != kNegInf;
   const float c2s = a.s.scale2, c2t = a.t.scale2;
   f32x16 dq[NDB];
 #pragma unroll
@@ -352,39 +420,41 @@ __global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) 
   const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
   const u16* kt_base = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh;
   const u16* kst_base = f.xT + ((int64_t)b * a.s.hkv + hs) * a.s.dim * (int64_t)f.Tp;
+  const unsigned char* tok = f.tok_ok + (int64_t)b * f.Tp;
 
-  const int nkt_all = (T + kTile - 1) / kTile;
-  const int ntiles = causal ? min(nkt_all, (row0 + ROWS - 1) / kTile + 1) : nkt_all;
-  auto issue_tile = [&](int t, int buf) {
+  const int nkt_all = f.Tp / kTile;
+  const int ntiles = causal ? min(nkt_all, (row0 + kRows - 1) / kTile + 1) : nkt_all;
+  auto issue_tile = [&](int t) {
+    const int buf = t % kStages;
     const int j0 = t * kTile;
-    issue_rows<DP, kDqWaves>(lks[buf], ks_base, a.s.k_st, j0, T, a.s.dim, w, lane);
-    issue_rows<DP, kDqWaves>(lkt[buf], kt_base, a.t.k_st, j0, T, a.t.dim, w, lane);
-    issue_tr<DP, kDqWaves>(lkst[buf], kst_base, f.Tp, j0, a.s.dim, w, lane);
-  };
-  auto col_ok = [&](int t) -> int {
-    const int j = t * kTile + tid;
-    return (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
+    issue_rows<DP>(lks[buf], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+    issue_rows<DP>(lkt[buf], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    issue_tr<DP>(lkst[buf], kst_base, f.Tp, j0, a.s.dim, w, lane);
+    issue_small(ltok[buf][w], tok + j0, lane);
   };
 
-  issue_tile(0, 0);
-  int next_ok = tid < kTile ? col_ok(0) : 1;
-  wait_all_memory();
-  if (tid < kTile) lcolok[0][tid] = next_ok;
-  int tile_masked = __syncthreads_or(!next_ok);
+  // The register operands loaded above must have landed before the ring
+  // starts: the compiler does not count the asm copies, so a wait it placed
+  // for these loads inside the loop would be vmcnt(0) and drain the ring.
+  wait_vmcnt<0>();
+  issue_tile(0);
+  if (ntiles > 1) issue_tile(1);
+  if (TC::kUniform && ntiles > 1)
+    wait_vmcnt<kPerWave>();
+  else
+    wait_vmcnt<0>();
+  __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) {
-      issue_tile(t + 1, buf ^ 1);
-      next_ok = tid < kTile ? col_ok(t + 1) : 1;
-    } else {
-      next_ok = 1;
-    }
+    const int buf = t % kStages;
+    const bool more = t + 2 < ntiles;
+    if (more) issue_tile(t + 2);
+    const bool col_masked = __any(ltok[buf][w][lane] == 0);
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const int gsb = 2 * t + sb;
       if (causal && gsb > diag_sb) continue;
-      const bool masked = tile_masked || (causal && gsb == diag_sb);
+      const bool masked = col_masked || (causal && gsb == diag_sb);
       f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
@@ -398,7 +468,7 @@ __global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) 
         float dd = fast_exp2(fmaf(ss[r], c2s, nls2)) - fast_exp2(fmaf(st[r], c2t, nlt2));
         if (masked) {
           const int jj = 32 * sb + 8 * (r >> 2) + 4 * half + (r & 3);
-          dd = (lcolok[buf][jj] && (!causal || t * kTile + jj <= my_i)) ? dd : 0.f;
+          dd = (ltok[buf][w][jj] && (!causal || t * kTile + jj <= my_i)) ? dd : 0.f;
         }
         dv[r] = to_bits(dd, BF);  // D cast to the input dtype (kernel_C.py:233)
       }
@@ -411,9 +481,11 @@ __global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) 
           dq[db] = mfma32<BF>(*reinterpret_cast<const u16x8*>(tr_chunk(lkst[buf], 32 * db + l32, c)), bop, dq[db]);
       }
     }
-    wait_all_memory();
-    if (t + 1 < ntiles && tid < kTile) lcolok[buf ^ 1][tid] = next_ok;
-    tile_masked = __syncthreads_or(!next_ok);
+    if (TC::kUniform && more)
+      wait_vmcnt<kPerWave>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
   }
 
   if (in_range) {
@@ -432,22 +504,25 @@ __global__ __launch_bounds__(kDqWaves * 64) void hot_dq_kernel(const HotArgs f) 
     }
   }
 }
+
 // ----------------------------------------------------------------------------
-// backward
+// backward, column side: dk = sm_scale_s sum_{h in group} D^T Q_s
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
-__global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArgs f) {
+__global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f) {
   const RelArgs& a = f.r;
-  constexpr int NT = kBwdWaves * 64;
+  using TC = TileCopies<DP>;
+  constexpr int NT = kWaves * 64;
   constexpr int KS = DP / 16;
   constexpr int TRR = DP < 32 ? 32 : DP;
   constexpr int NDB = TRR / 32;
-  constexpr int COLS = kBwdWaves * 32;
-  __shared__ __attribute__((aligned(16))) u16 lqs[2][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lqt[2][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lqst[2][TRR * kTile];
-  __shared__ __attribute__((aligned(16))) float llse_s[2][kTile];  // log2 units, +inf = row excluded
-  __shared__ __attribute__((aligned(16))) float llse_t[2][kTile];
+  constexpr int kPerWave = 2 * TC::kRowPerWave + TC::kTrPerWave + 1;
+  __shared__ __attribute__((aligned(16))) u16 lqs[kStages][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lqt[kStages][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lqst[kStages][TRR * kTile];
+  // per query row of the tile: -lse*log2(e) of student [0, 64) and teacher [64, 128)
+  __shared__ __attribute__((aligned(16))) float lnl[kStages][2 * kTile];
+  static_assert(2 * kTile * sizeof(float) == kWaves * 64, "one 64-byte row-data copy per wave");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -455,11 +530,13 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int T = a.T;
-  const int cb = blockIdx.x;  // small cb = longest causal columns, launched first
-  const int bg = blockIdx.y;
+  const int ncb = (T + kRows - 1) / kRows;
+  const int item = xcd_item(blockIdx.x, ncb * a.B * a.s.hkv);
+  const int bg = item / ncb;
+  const int cb = item - bg * ncb;  // small cb = longest causal columns first
   const int b = bg / a.s.hkv;
   const int g = bg - b * a.s.hkv;
-  const int j0w = cb * COLS + w * 32;
+  const int j0w = cb * kRows + w * 32;
   const int my_j = j0w + l32;
   const bool in_range = my_j < T;
   const bool col_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_j);
@@ -467,7 +544,7 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
   const int diag_sb = j0w >> 5;  // the 32-row sub-block holding this wave's diagonal
 
   if constexpr (DP < 32) {
-    for (int c = tid; c < 2 * TRR * kTile; c += NT) {
+    for (int c = tid; c < kStages * TRR * kTile; c += NT) {
       const int buf = c / (TRR * kTile), e = c % (TRR * kTile);
       if (e >= DP * kTile) lqst[buf][e] = 0;
     }
@@ -487,8 +564,8 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
   for (int db = 0; db < NDB; ++db) dk[db] = (f32x16)(0.f);
 
   const float c2s = a.s.scale2, c2t = a.t.scale2;
-  const int ntile_all = (T + kTile - 1) / kTile;
-  const int it0 = causal ? (cb * COLS) / kTile : 0;
+  const int ntile_all = f.Tp / kTile;
+  const int it0 = causal ? (cb * kRows) / kTile : 0;
   int loaded_ht = -1;
 
   for (int hh = 0; hh < a.s.group; ++hh) {
@@ -507,45 +584,31 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
     const u16* qs_base = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh;
     const u16* qt_base = a.t.q + (int64_t)b * a.t.q_sb + (int64_t)h * a.t.q_sh;
     const u16* qst_base = f.xT + bh * a.s.dim * (int64_t)f.Tp;
+    // wave w copies 16 normalisers: student rows 16w.. (w < 4), teacher rows 16(w-4).. (w >= 4)
+    const float* nl_src = (w < 4 ? f.nl_s : f.nl_t) + bh * f.Tp + 16 * (w & 3);
 
-    auto issue_tile = [&](int t, int buf) {
+    auto issue_tile = [&](int t) {
+      const int buf = (t - it0) % kStages;
       const int i0 = t * kTile;
-      issue_rows<DP, kBwdWaves>(lqs[buf], qs_base, a.s.q_st, i0, T, a.s.dim, w, lane);
-      issue_rows<DP, kBwdWaves>(lqt[buf], qt_base, a.t.q_st, i0, T, a.t.dim, w, lane);
-      issue_tr<DP, kBwdWaves>(lqst[buf], qst_base, f.Tp, i0, a.s.dim, w, lane);
-    };
-    // Row data: log2-domain LSE, +inf for rows outside the valid set so that
-    // exp2(x - inf) = 0 removes them without per-element tests.
-    auto row_data = [&](int t, float& o_s, float& o_t) {
-      const int i = t * kTile + tid;
-      float ls = 0.f, lt = 0.f;
-      bool rv = false;
-      if (i < T) {
-        rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + i);
-        ls = a.lse_s_in[bh * T + i];
-        lt = a.lse_t_in[bh * T + i];
-      }
-      const bool ok = rv && ls != kNegInf && lt != kNegInf;
-      o_s = ok ? ls * kLog2e : __builtin_inff();
-      o_t = ok ? lt * kLog2e : __builtin_inff();
+      issue_rows<DP>(lqs[buf], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
+      issue_rows<DP>(lqt[buf], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
+      issue_tr<DP>(lqst[buf], qst_base, f.Tp, i0, a.s.dim, w, lane);
+      issue_small(&lnl[buf][16 * w], nl_src + i0, lane);
     };
 
-    float nls = 0.f, nlt = 0.f;
-    issue_tile(it0, 0);
-    if (tid < kTile) row_data(it0, nls, nlt);
-    wait_all_memory();
-    if (tid < kTile) {
-      llse_s[0][tid] = nls;
-      llse_t[0][tid] = nlt;
-    }
+    wait_vmcnt<0>();  // teacher key fragments landed before the ring starts
+    issue_tile(it0);
+    if (it0 + 1 < ntile_all) issue_tile(it0 + 1);
+    if (TC::kUniform && it0 + 1 < ntile_all)
+      wait_vmcnt<kPerWave>();
+    else
+      wait_vmcnt<0>();
     __syncthreads();
 
     for (int t = it0; t < ntile_all; ++t) {
-      const int buf = (t - it0) & 1;
-      if (t + 1 < ntile_all) {
-        issue_tile(t + 1, buf ^ 1);
-        if (tid < kTile) row_data(t + 1, nls, nlt);
-      }
+      const int buf = (t - it0) % kStages;
+      const bool more = t + 2 < ntile_all;
+      if (more) issue_tile(t + 2);
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int gsb = 2 * t + sb;
@@ -562,12 +625,12 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int ii0 = 32 * sb + 8 * r4 + 4 * half;
-          const f32x4 ls4 = *reinterpret_cast<const f32x4*>(&llse_s[buf][ii0]);
-          const f32x4 lt4 = *reinterpret_cast<const f32x4*>(&llse_t[buf][ii0]);
+          const f32x4 ls4 = *reinterpret_cast<const f32x4*>(&lnl[buf][ii0]);
+          const f32x4 lt4 = *reinterpret_cast<const f32x4*>(&lnl[buf][kTile + ii0]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * r4 + e;
-            float dd = fast_exp2(fmaf(ss[r], c2s, -ls4[e])) - fast_exp2(fmaf(st[r], c2t, -lt4[e]));
+            float dd = fast_exp2(fmaf(ss[r], c2s, ls4[e])) - fast_exp2(fmaf(st[r], c2t, lt4[e]));
             if (diag) dd = (t * kTile + ii0 + e >= my_j) ? dd : 0.f;
             dv[r] = to_bits(dd, BF);  // D cast to the input dtype (kernel_C.py:233)
           }
@@ -581,11 +644,10 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
             dk[db] = mfma32<BF>(*reinterpret_cast<const u16x8*>(tr_chunk(lqst[buf], 32 * db + l32, c)), bop, dk[db]);
         }
       }
-      wait_all_memory();
-      if (t + 1 < ntile_all && tid < kTile) {
-        llse_s[buf ^ 1][tid] = nls;
-        llse_t[buf ^ 1][tid] = nlt;
-      }
+      if (TC::kUniform && more)
+        wait_vmcnt<kPerWave>();
+      else
+        wait_vmcnt<0>();
       __syncthreads();
     }
   }
@@ -612,13 +674,16 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void hot_bwd_kernel(const HotArg
   }
 }
 
-// Transposed, key-permuted copy of x for the second GEMM of both kernels.
+// Transposed, key-permuted copy of x for the second GEMM of both backward kernels.
 __global__ void transpose_keys_kernel(const u16* __restrict__ x, int64_t sb, int64_t sh, int64_t st, int H, int T,
                                       int D, int Tp, u16* __restrict__ xT);
 
 bool hot_supported(int ds, int dt, bool same_dtype);
 hipError_t launch_transpose_keys(const u16* x, int64_t sb, int64_t sh, int64_t st, int B, int H, int T, int D, int Tp,
                                  u16* xT, hipStream_t stream);
+hipError_t launch_token_prep(const RelArgs& a, int Tp, unsigned char* tok_ok, hipStream_t stream);
+hipError_t launch_row_prep(const RelArgs& a, int Tp, const unsigned char* tok_ok, float* nl_s, float* nl_t,
+                           hipStream_t stream);
 hipError_t launch_hot_fwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
 hipError_t launch_hot_dq(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
 hipError_t launch_hot_bwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);

@@ -415,6 +415,8 @@ hipError_t launch_row_lse(const RelArgs& a, int dps, hipStream_t stream);
 hipError_t launch_row_kl(const RelArgs& a, int dps, int dpt, hipStream_t stream);
 hipError_t launch_row_dq(const RelArgs& a, int dps, int dpt, hipStream_t stream);
 hipError_t launch_col_dk(const RelArgs& a, int dps, int dpt, hipStream_t stream);
-hipError_t launch_reduce_sum(const float* x, int64_t n, float* out, hipStream_t stream);
+// Loss reduction: out = sum(x[0..n)) through kReduceBlocks double partials.
+constexpr int kReduceBlocks = 512;
+hipError_t launch_reduce_sum(const float* x, int64_t n, double* partial, float* out, hipStream_t stream);
 
 }  // namespace lard

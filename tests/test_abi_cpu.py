@@ -55,8 +55,20 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     m.kind = 0
     rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, float("nan"), 64, None)
     assert rc == -1 and b"sm_scale" in L.lard_last_error()
-    assert L.lard_kl_forward_workspace_bytes(2, 3, 5) == 2 * 3 * 5 * 4
+    # per-row KL terms (256-byte aligned) + 512 double partials of the loss sum
+    assert L.lard_kl_forward_workspace_bytes(2, 3, 5) == 256 + 512 * 8
+    assert L.lard_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8
     assert L.lard_kl_forward_workspace_bytes(0, 3, 5) == 0
+    # forward of the autograd path adds one validity byte per (padded) token
+    assert L.lard_attn_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8 + 4 * 4096
+    # backward: transposed keys (+ queries unless q is k), validity, 2 normalisers per row
+    B, H, T, D = 2, 8, 1000, 64
+    Tp = 1024
+    kt = B * H * D * Tp * 2
+    tail = B * Tp + 2 * B * H * Tp * 4
+    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 1) == kt + tail
+    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 0) == 2 * kt + tail
+    assert L.lard_attn_kl_backward_workspace_bytes(0, H, H, T, D, 0) == 0
 
 
 def test_python_wrappers_reject_cpu_tensors():
