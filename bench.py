@@ -9,10 +9,20 @@ torch.Generator and are resident in HBM before timing starts.
 
 Printed metric: relation-tokens/s (one relation-token = one (b, h, i) row,
 train.py:404), whole job.  Extra fields carry TFLOP/s against the
-algorithmic 12*d*P flop count, the roofline of the dominant kernel (timed
-live with HIP events on the launch stream), peak HBM, and a CPU baseline:
-the oracle's linear-memory float32 restatement run on this host for one
-(b, h) relation, scaled to the same unit.
+algorithmic 12*d*P flop count, the roofline of the dominant kernel, peak
+HBM, and a CPU baseline: the oracle's linear-memory float32 restatement run
+on this host for one (b, h) relation, scaled to the same unit.
+
+Roofline: the library's timing hook (lard_timing_*) brackets each launch of
+its three kernels with HIP events on the launch stream during the timed
+steps.  Each kernel is credited 4*d*P algorithmic flops per (b, h): the
+forward owns S_s and S_t (2 GEMMs), each backward kernel owns one of the two
+gradient products (D.K_s, D^T.Q_s) plus half of the S_s, S_t recompute.  The
+dominant kernel is the one with the longest average launch.  `traffic` (HBM
+bytes per launch of that kernel) comes from the counter summary
+profiles/traffic_<config>.json when present (rocprofv3 FETCH_SIZE and
+WRITE_SIZE runs of this script with --copy-calibration, scaled by a plain
+copy of known size), else null.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg4]
 """
@@ -20,6 +30,7 @@ the oracle's linear-memory float32 restatement run on this host for one
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -96,6 +107,18 @@ def cpu_baseline(n, d, relations):
 
 
 
+KERNELS = ("forward", "row_grad", "col_grad")
+
+
+def traffic_summary(config):
+    """HBM bytes per launch per kernel from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path, "r", encoding="utf-8") as f:
+        return json.load(f)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -103,6 +126,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB first (counter-scale calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -112,6 +137,7 @@ def main():
 
     import torch
 
+    from linearard_amd import _lib
     from linearard_amd.attention_KL import attn_kl_align
 
     B, H, n, d, pos_scale, base = CONFIGS[args.config]
@@ -154,16 +180,36 @@ def main():
             ev["bwd"].append((marks["b0"], marks["b1"]))
         return loss
 
+    if args.copy_calibration > 0:
+        # a streaming copy of known size: reads and writes exactly nbytes once
+        nbytes = args.copy_calibration << 20
+        src = torch.ones(nbytes // 4, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+
+    L = _lib.lib()
     base_mem = torch.cuda.memory_allocated(dev)
     torch.cuda.reset_peak_memory_stats(dev)
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
+    _lib.check(L.lard_timing_enable(1), "lard_timing_enable")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         loss = step(True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    _lib.check(L.lard_timing_enable(0), "lard_timing_enable")
+    kernel_ms = {}
+    for name in KERNELS:
+        total = ctypes.c_double()
+        count = ctypes.c_int64()
+        _lib.check(L.lard_timing_read(_lib.KERNEL_IDS[name], ctypes.byref(total), ctypes.byref(count)),
+                   "lard_timing_read")
+        if count.value:
+            kernel_ms[name] = total.value / count.value
     peak = torch.cuda.max_memory_allocated(dev) - base_mem
 
     fwd_ms = sum(a.elapsed_time(b) for a, b in ev["fwd"]) / len(ev["fwd"])
@@ -171,11 +217,15 @@ def main():
     ms = elapsed / args.steps * 1e3
     flops = algorithmic_flops(B, H, n, d)
     rows = B * H * n
-    # Each phase is credited half of the 12 d P algorithmic flops: the forward
-    # owns S_s, S_t (4dP) plus the row-side D.X product (2dP); the backward
-    # owns the S_s, S_t recompute (4dP) plus D^T.X (2dP).
-    dom_name, dom_ms = ("backward", bwd_ms) if bwd_ms >= fwd_ms else ("forward", fwd_ms)
-    achieved = (flops / 2) / (dom_ms * 1e-3) / 1e12
+    # 4 d P algorithmic flops per (b, h) for each of the three kernels.
+    per_launch = flops / 3
+    dom_name = max(kernel_ms, key=kernel_ms.get)
+    dom_ms = kernel_ms[dom_name]
+    achieved = per_launch / (dom_ms * 1e-3) / 1e12
+    summary = traffic_summary(args.config)
+    traffic = None
+    if summary is not None and dom_name in summary.get("bytes_per_launch", {}):
+        traffic = summary["bytes_per_launch"][dom_name]
 
     out = {
         "metric": "attention-KL fwd+bwd relation-tokens/sec at n=32K, d=128",
@@ -195,11 +245,13 @@ def main():
         "tflops": flops / (ms * 1e-3) / 1e12,
         "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS,
         "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
+        "kernel_ms": kernel_ms,
         "peak_hbm_bytes": int(peak),
         "loss": float(loss.item()),
         "roofline": {"bound": "mfma", "kernel": dom_name, "achieved": achieved,
                      "peak": MI355X_BF16_DENSE_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / MI355X_BF16_DENSE_TFLOPS, "traffic": None},
+                     "frac": achieved / MI355X_BF16_DENSE_TFLOPS, "traffic": traffic,
+                     "flop_per_launch": per_launch, "avg_launch_ms": dom_ms},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -75,7 +75,8 @@ const char* lard_last_error(void);
 int lard_lse_stats(const lard_tensor4* q, const lard_tensor4* k, const lard_mask* mask,
                    int causal, float sm_scale, float* lse_out, void* stream);
 
-/* Workspace needed by lard_kl_forward for B x Hq x T rows (bytes). */
+/* Workspace needed by lard_kl_forward for B x Hq x T rows (bytes): the
+ * per-row KL terms and the partials of the fixed-order loss sum. */
 size_t lard_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len);
 
 /*
@@ -102,7 +103,8 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
                      const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
                      float* dq_out, float* dk_out, void* stream);
 
-/* Workspace needed by lard_attn_kl_forward (bytes): the per-row KL terms. */
+/* Workspace needed by lard_attn_kl_forward (bytes): the per-row KL terms,
+ * the loss-sum partials and one validity byte per token. */
 size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len);
 
 /*
@@ -118,7 +120,8 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace needed by lard_attn_kl_backward (bytes): transposed copies of ks
- * and (unless self_relation) qs. */
+ * and (unless self_relation) qs, one validity byte per token and the two
+ * log2-domain row normalisers per query row. */
 size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,
                                              int64_t head_dim, int self_relation);
 
@@ -139,6 +142,26 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                           const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
                           const float* dloss, int self_relation, float* dq_out, float* dk_out,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel ids of the timing hook. */
+#define LARD_KERNEL_FORWARD 0  /* one-pass forward: both LSEs and the per-row KL */
+#define LARD_KERNEL_ROW_GRAD 1 /* backward, row side: dq (kernel_C.py:224-239) */
+#define LARD_KERNEL_COL_GRAD 2 /* backward, column side: dk (kernel_C.py:242-253) */
+#define LARD_KERNEL_COUNT 3
+
+/*
+ * Timing hook for measurement harnesses -- no counterpart in the reference
+ * (its kernels are timed from outside).  While enabled, every launch of the
+ * three kernels above by lard_attn_kl_forward / lard_attn_kl_backward /
+ * lard_kl_backward is bracketed by two HIP events recorded on its launch
+ * stream.  lard_timing_read() waits for the recorded events and returns the
+ * summed elapsed milliseconds and the launch count of one kernel since its
+ * last read, then clears them.  Off by default.  While enabled, launches
+ * cannot be captured into a HIP graph and calls from several host threads
+ * serialise briefly on one lock.
+ */
+int lard_timing_enable(int on);
+int lard_timing_read(int kernel, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus
 }

@@ -68,7 +68,12 @@ SIGNATURES = {
     "lard_attn_kl_backward": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, _FP, ctypes.c_int, _FP, _FP, ctypes.c_void_p,
                                              ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_timing_enable": (ctypes.c_int, [ctypes.c_int]),
+    "lard_timing_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_int64)]),
 }
+
+KERNEL_IDS = {"forward": 0, "row_grad": 1, "col_grad": 2}
 
 _LIB = None
 

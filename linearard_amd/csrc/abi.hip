@@ -11,6 +11,9 @@
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
+#include <utility>
+#include <vector>
 #include <string>
 
 #include "../../include/linearard_amd.h"
@@ -245,9 +248,92 @@ BwdWs bwd_layout(void* base, int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int6
   return w;
 }
 
+// Opt-in launch timing (lard_timing_*): event pairs recorded around the
+// throughput launches, drained by lard_timing_read.  Events are pooled and
+// never destroyed, so a read never races a record on another thread.
+struct Timing {
+  std::mutex mu;
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[LARD_KERNEL_COUNT];
+  std::vector<hipEvent_t> pool;
+
+  hipEvent_t take() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+  }
+};
+
+Timing& timing() {
+  static Timing t;
+  return t;
+}
+
+// Runs launch() on stream st; brackets it with events when timing is on.
+template <class F>
+hipError_t timed(int kernel, hipStream_t st, F&& launch) {
+  Timing& tm = timing();
+  hipEvent_t start = nullptr;
+  {
+    std::lock_guard<std::mutex> g(tm.mu);
+    if (tm.on && (start = tm.take()) != nullptr && hipEventRecord(start, st) != hipSuccess) {
+      tm.pool.push_back(start);
+      start = nullptr;
+    }
+  }
+  const hipError_t e = launch();
+  if (start != nullptr) {
+    std::lock_guard<std::mutex> g(tm.mu);
+    hipEvent_t stop = tm.take();
+    if (stop != nullptr && hipEventRecord(stop, st) == hipSuccess) {
+      tm.pending[kernel].emplace_back(start, stop);
+    } else {
+      tm.pool.push_back(start);
+      if (stop != nullptr) tm.pool.push_back(stop);
+    }
+  }
+  return e;
+}
+
 }  // namespace
 
 extern "C" {
+
+int lard_timing_enable(int on) {
+  Timing& tm = timing();
+  std::lock_guard<std::mutex> g(tm.mu);
+  tm.on = on != 0;
+  return ok();
+}
+
+int lard_timing_read(int kernel, double* total_ms, int64_t* launches) {
+  if (kernel < 0 || kernel >= LARD_KERNEL_COUNT) return fail(LARD_ERR_INVALID_ARGUMENT, "unknown kernel id %d", kernel);
+  if (total_ms == nullptr || launches == nullptr)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "total_ms / launches must not be NULL");
+  Timing& tm = timing();
+  std::lock_guard<std::mutex> g(tm.mu);
+  double sum = 0.0;
+  int64_t n = 0;
+  hipError_t err = hipSuccess;
+  for (auto& pr : tm.pending[kernel]) {
+    float ms = 0.f;
+    if (err == hipSuccess) err = hipEventSynchronize(pr.second);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, pr.first, pr.second);
+    sum += ms;
+    ++n;
+    tm.pool.push_back(pr.first);
+    tm.pool.push_back(pr.second);
+  }
+  tm.pending[kernel].clear();
+  *total_ms = sum;
+  *launches = n;
+  return hip_status(err, "timing read");
+}
+
 
 const char* lard_version(void) { return "linearard_amd 0.1.0 gfx950"; }
 
@@ -326,8 +412,11 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
   a.dq_out = dq_out;
   a.dk_out = dk_out;
   const int dps = padded_dim(qs->size[3]), dpt = padded_dim(qt->size[3]);
-  if ((rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "kl_backward dq launch")) != LARD_OK) return rc;
-  return hip_status(lard::launch_col_dk(a, dps, dpt, st), "kl_backward dk launch");
+  if ((rc = hip_status(timed(LARD_KERNEL_ROW_GRAD, st, [&] { return lard::launch_row_dq(a, dps, dpt, st); }),
+                       "kl_backward dq launch")) != LARD_OK)
+    return rc;
+  return hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_col_dk(a, dps, dpt, st); }),
+                    "kl_backward dk launch");
 }
 
 size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
@@ -380,14 +469,16 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
         if ((rc = hip_status(lard::launch_token_prep(f.r, f.Tp, w.tok_ok, st),
                              "attn_kl_forward token prep launch")) != LARD_OK)
           return rc;
-        rc = hip_status(lard::launch_hot_fwd(f, padded_dim(ds), bf, st), "attn_kl_forward launch");
+        rc = hip_status(timed(LARD_KERNEL_FORWARD, st, [&] { return lard::launch_hot_fwd(f, padded_dim(ds), bf, st); }),
+                        "attn_kl_forward launch");
       } else {
         lard::FusedArgs g{};
         g.r = f.r;
         g.lse_s_out = lse_s_out;
         g.lse_t_out = lse_t_out;
         g.row_out = f.row_out;
-        rc = hip_status(lard::launch_fused_fwd(g, padded_dim(ds), bf, st), "attn_kl_forward fused launch");
+        rc = hip_status(timed(LARD_KERNEL_FORWARD, st, [&] { return lard::launch_fused_fwd(g, padded_dim(ds), bf, st); }),
+                        "attn_kl_forward fused launch");
       }
       if (rc != LARD_OK) return rc;
     } else {
@@ -479,24 +570,28 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
     f.nl_t = w.nl_t;
     f.dq_out = dq_dst;
     f.r.dscale = self_relation ? nullptr : dloss;
-    if ((rc = hip_status(lard::launch_hot_dq(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, st),
+    const bool bf = qs->dtype == LARD_DTYPE_BF16;
+    if ((rc = hip_status(timed(LARD_KERNEL_ROW_GRAD, st, [&] { return lard::launch_hot_dq(f, padded_dim(ds), bf, st); }),
                          "attn_kl_backward dq launch")) != LARD_OK)
       return rc;
     f.xT = w.qT;
     f.r.dk_out = dk_out;
     f.r.dk_add = self_relation ? dk_out : nullptr;
     f.r.dscale = dloss;
-    return hip_status(lard::launch_hot_bwd(f, padded_dim(ds), qs->dtype == LARD_DTYPE_BF16, st),
+    return hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_hot_bwd(f, padded_dim(ds), bf, st); }),
                       "attn_kl_backward dk launch");
   }
   const int dps = padded_dim(ds), dpt = padded_dim(dt);
   a.dq_out = dq_dst;
   a.dscale = self_relation ? nullptr : dloss;
-  if ((rc = hip_status(lard::launch_row_dq(a, dps, dpt, st), "attn_kl_backward dq launch")) != LARD_OK) return rc;
+  if ((rc = hip_status(timed(LARD_KERNEL_ROW_GRAD, st, [&] { return lard::launch_row_dq(a, dps, dpt, st); }),
+                       "attn_kl_backward dq launch")) != LARD_OK)
+    return rc;
   a.dk_out = dk_out;
   a.dk_add = self_relation ? dk_out : nullptr;
   a.dscale = dloss;
-  return hip_status(lard::launch_col_dk(a, dps, dpt, st), "attn_kl_backward dk launch");
+  return hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_col_dk(a, dps, dpt, st); }),
+                    "attn_kl_backward dk launch");
 }
 
 }  // extern "C"

@@ -565,7 +565,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
 
   const float c2s = a.s.scale2, c2t = a.t.scale2;
   const int ntile_all = f.Tp / kTile;
-  const int it0 = causal ? (cb * kRows) / kTile : 0;
+  // Query tiles run from the last one down to this block's diagonal: all
+  // workgroups in flight then read the same tile at the same time (one L2
+  // fill serves the XCD), instead of each starting at its own diagonal.
+  const int ntiles = causal ? ntile_all - (cb * kRows) / kTile : ntile_all;
+  auto tile_of = [&](int it) { return ntile_all - 1 - it; };
   int loaded_ht = -1;
 
   for (int hh = 0; hh < a.s.group; ++hh) {
@@ -587,9 +591,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
     // wave w copies 16 normalisers: student rows 16w.. (w < 4), teacher rows 16(w-4).. (w >= 4)
     const float* nl_src = (w < 4 ? f.nl_s : f.nl_t) + bh * f.Tp + 16 * (w & 3);
 
-    auto issue_tile = [&](int t) {
-      const int buf = (t - it0) % kStages;
-      const int i0 = t * kTile;
+    auto issue_tile = [&](int it) {
+      const int buf = it % kStages;
+      const int i0 = tile_of(it) * kTile;
       issue_rows<DP>(lqs[buf], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
       issue_rows<DP>(lqt[buf], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
       issue_tr<DP>(lqst[buf], qst_base, f.Tp, i0, a.s.dim, w, lane);
@@ -597,18 +601,19 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
     };
 
     wait_vmcnt<0>();  // teacher key fragments landed before the ring starts
-    issue_tile(it0);
-    if (it0 + 1 < ntile_all) issue_tile(it0 + 1);
-    if (TC::kUniform && it0 + 1 < ntile_all)
+    issue_tile(0);
+    if (ntiles > 1) issue_tile(1);
+    if (TC::kUniform && ntiles > 1)
       wait_vmcnt<kPerWave>();
     else
       wait_vmcnt<0>();
     __syncthreads();
 
-    for (int t = it0; t < ntile_all; ++t) {
-      const int buf = (t - it0) % kStages;
-      const bool more = t + 2 < ntile_all;
-      if (more) issue_tile(t + 2);
+    for (int it = 0; it < ntiles; ++it) {
+      const int buf = it % kStages;
+      const int t = tile_of(it);
+      const bool more = it + 2 < ntiles;
+      if (more) issue_tile(it + 2);
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int gsb = 2 * t + sb;

@@ -119,3 +119,41 @@ def test_drop_in_shim_names():
     assert kernel_C.kl_backward_triton is kernel_C.kl_backward
     assert kernel_A.SUPPORTED_HEAD_DIMS == (8, 16, 32, 64, 128, 256)
     assert callable(attn_kl_align) and issubclass(AttnKLAlignFn, torch.autograd.Function)
+
+
+def test_timing_hook_validates_and_reads_empty_without_a_gpu():
+    L = _lib.lib()
+    total = ctypes.c_double(-1.0)
+    count = ctypes.c_int64(-1)
+    assert L.lard_timing_read(7, ctypes.byref(total), ctypes.byref(count)) == -1
+    assert b"kernel id" in L.lard_last_error()
+    assert L.lard_timing_read(0, None, ctypes.byref(count)) == -1
+    assert L.lard_timing_enable(0) == 0
+    for kid in _lib.KERNEL_IDS.values():  # nothing recorded: no HIP call is made
+        assert L.lard_timing_read(kid, ctypes.byref(total), ctypes.byref(count)) == 0
+        assert total.value == 0.0 and count.value == 0
+
+
+def test_counter_summary_scales_by_the_calibration_copy(tmp_path):
+    from linearard_amd import profiling
+
+    head = ("Correlation_Id,Dispatch_Id,Agent_Id,Queue_Id,Process_Id,Thread_Id,Grid_Size,Kernel_Id,Kernel_Name,"
+            "Workgroup_Size,LDS_Block_Size,Scratch_Size,VGPR_Count,Accum_VGPR_Count,SGPR_Count,Counter_Name,"
+            "Counter_Value,Start_Timestamp,End_Timestamp\n")
+
+    def row(d, name, counter, v):
+        return f'{d},{d},A,1,1,1,1,1,"{name}",256,0,0,8,0,8,{counter},{v},0,1\n'
+
+    fetch = tmp_path / "f.csv"
+    write = tmp_path / "w.csv"
+    # the calibration copy of 1 MiB reads as 512 counts (2 KiB per count); two
+    # launches of the column kernel read 3000 and 1000 counts (mean 2000)
+    fetch.write_text(head + row(1, "void at::native::neg_kernel_cuda(x)", "FETCH_SIZE", 512)
+                     + row(2, "void lard::hot_bwd_kernel<128, true>(lard::HotArgs)", "FETCH_SIZE", 3000)
+                     + row(3, "void lard::hot_bwd_kernel<128, true>(lard::HotArgs)", "FETCH_SIZE", 1000))
+    write.write_text(head + row(1, "void at::native::neg_kernel_cuda(x)", "WRITE_SIZE", 1024)
+                     + row(2, "void lard::hot_bwd_kernel<128, true>(lard::HotArgs)", "WRITE_SIZE", 100))
+    out = profiling.traffic(str(fetch), str(write), 1, "cfg4")
+    assert out["scale_fetch_bytes_per_count"] == 2048.0 and out["scale_write_bytes_per_count"] == 1024.0
+    assert out["read_bytes"]["col_grad"] == 2000 * 2048.0
+    assert out["bytes_per_launch"]["col_grad"] == 2000 * 2048.0 + 100 * 1024.0
