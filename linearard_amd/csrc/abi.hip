@@ -453,7 +453,11 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
     const bool same = qs->dtype == qt->dtype;
     const bool bf = qs->dtype == LARD_DTYPE_BF16;
     const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
-    const bool hot = lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T);
+    // the throughput forward keeps masked logits at -1e30 raw units: scales
+    // must be nonzero and moderate (|scale| <= 1e6) for that to stay exact
+    const bool scales_ok = sm_scale_s != 0.f && sm_scale_t != 0.f && std::fabs(sm_scale_s) <= 1e6f &&
+                           std::fabs(sm_scale_t) <= 1e6f;
+    const bool hot = lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T) && scales_ok;
     if (hot || lard::fused_fwd_supported(ds, dt, same)) {
       lard::HotArgs f{};
       fill_side(f.r.s, qs, ks, Hq, sm_scale_s);

@@ -91,8 +91,9 @@ __device__ __forceinline__ void lds_async16(const void* base, unsigned voff, voi
 // (expcnt / lgkmcnt fields left at their maxima).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  // gfx9 encoding: vmcnt = simm16[15:14]:[3:0], expcnt [6:4], lgkmcnt [11:8]
+  __builtin_amdgcn_s_waitcnt(0xF70 | (N & 15) | ((N >> 4) << 14));
 }
 
 // Position of workgroup `bid` in a work list of n items after the XCD-aware
@@ -120,13 +121,13 @@ __device__ __forceinline__ const u16* tr_chunk(const u16* tile, int d, int c) {
 // Copies per wave per tile.  They are uniform across waves when the chunk
 // count of a tile is a multiple of the wave count (D >= 64); otherwise the
 // kernels wait for everything (vmcnt 0) and lose only the look-ahead.
-template <int DP>
+template <int DP, int NW = kWaves>
 struct TileCopies {
   static constexpr int kRowInst = kTile * (DP / 8) / 64;  // per row tile
   static constexpr int kTrInst = DP * 8 / 64;             // per transposed tile
-  static constexpr bool kUniform = kRowInst % kWaves == 0;
-  static constexpr int kRowPerWave = kRowInst / kWaves;
-  static constexpr int kTrPerWave = kTrInst / kWaves;
+  static constexpr bool kUniform = kRowInst % NW == 0;
+  static constexpr int kRowPerWave = kRowInst / NW;
+  static constexpr int kTrPerWave = kTrInst / NW;
 };
 
 // Issue the async copy of rows [row0, row0 + kTile) x [0, DP) of one head
@@ -135,13 +136,17 @@ struct TileCopies {
 // every consumer zeroes or masks their contribution (key rows >= T are
 // invalid tokens, query rows >= T have -inf normalisers, padded columns meet
 // zero register operands).  The host keeps every offset below 2^31 bytes.
-template <int DP>
+template <int DP, int NW = kWaves>
 __device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_stride, int row0, int T, int dim,
                                            int wave, int lane) {
   constexpr int CPR = DP / 8;
   constexpr int NINST = TileCopies<DP>::kRowInst;
+  // a compile-time trip count when the copies divide evenly (no branches)
+  constexpr int NITER = NINST % NW == 0 ? NINST / NW : (NINST + NW - 1) / NW;
 #pragma unroll
-  for (int n = wave; n < NINST; n += kWaves) {
+  for (int i = 0; i < NITER; ++i) {
+    const int n = wave + NW * i;
+    if (NINST % NW != 0 && n >= NINST) break;
     const int p = 64 * n + lane;
     const int r = p / CPR;
     int c = (p % CPR) ^ (r & (CPR - 1));
@@ -154,11 +159,14 @@ __device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_st
 // Issue the async copy of the transposed tile [DP][kTile] starting at key0
 // (srcT = one head of xT, rows Tp apart).  Rows d >= dim copy row 0: they
 // feed output columns that are never stored.
-template <int DP>
+template <int DP, int NW = kWaves>
 __device__ __forceinline__ void issue_tr(u16* tile, const u16* srcT, int Tp, int key0, int dim, int wave, int lane) {
   constexpr int NINST = TileCopies<DP>::kTrInst;
+  constexpr int NITER = NINST % NW == 0 ? NINST / NW : (NINST + NW - 1) / NW;
 #pragma unroll
-  for (int n = wave; n < NINST; n += kWaves) {
+  for (int i = 0; i < NITER; ++i) {
+    const int n = wave + NW * i;
+    if (NINST % NW != 0 && n >= NINST) break;
     const int p = 64 * n + lane;
     const int d = p >> 3;
     const int c = (p & 7) ^ ((d >> 1) & 7);
@@ -176,20 +184,105 @@ __device__ __forceinline__ u16x8 pack8(const u16* v) { return (u16x8){v[0], v[1]
 
 // ----------------------------------------------------------------------------
 // forward: both online softmaxes and the KL, one pass (2 GEMMs per pair)
+//
+// Softmax state: each lane keeps its own running maxima for its half of the
+// row's keys (lanes l and l+32 share a row), so the loop needs no cross-lane
+// exchange; the halves are merged once at the end.  The maxima are lazy (a
+// rescale only when a block max exceeds the running max by 2^8 in
+// probability), in raw logit units; a negative scale is handled by flipping
+// the sign of q (exact), so the effective scale is positive.  Masked elements
+// (causal diagonal, invalid keys) are set to -1e30 in place: with running
+// maxima starting at -5e29 their exponentials are exactly 0 and every product
+// stays finite.
 // ----------------------------------------------------------------------------
+constexpr float kMaskedLogit = -1e30f;  // raw logit of a masked element
+constexpr float kStartMax = -5e29f;     // running max before the first valid key
+
+// Online-softmax state of one query row for this lane's half of the keys.
+struct SoftRow {
+  float m_s, m_t;    // running maxima, raw (sign-corrected) logit units
+  float nm_s, nm_t;  // -m * c2 (log2 units)
+  float l_s, l_t;    // sums of exp2(x * c2 + nm)
+  float acc;         // sum of p_t * (ratio * st - ss)
+};
+
+// Set the invalid elements of a masked sub-block to kMaskedLogit.  Element r
+// of this lane is key (first + off(r)), off(r) = 8*(r/4) + r%4; it is valid
+// when bit off(r) of `bits` is set and (causal) off(r) <= lim = row - first.
+__device__ __forceinline__ void mask_block(f32x16& ss, f32x16& st, unsigned bits, int lim, bool causal) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int off = 8 * (r >> 2) + (r & 3);
+    const bool v = ((bits >> off) & 1u) && (!causal || off <= lim);
+    ss[r] = v ? ss[r] : kMaskedLogit;
+    st[r] = v ? st[r] : kMaskedLogit;
+  }
+}
+
+// Lazy max update: rescale the lane's sums when a block max exceeds the
+// running max by more than `thr` (raw units); uniform branch, rare.
+__device__ __forceinline__ void block_max(const f32x16& ss, const f32x16& st, SoftRow& R, float c2s, float c2t,
+                                          float thr_s, float thr_t) {
+  float mb_s = fmaxf(ss[0], ss[1]), mb_t = fmaxf(st[0], st[1]);
+#pragma unroll
+  for (int r = 2; r < 16; r += 2) {
+    mb_s = fmaxf(fmaxf(mb_s, ss[r]), ss[r + 1]);
+    mb_t = fmaxf(fmaxf(mb_t, st[r]), st[r + 1]);
+  }
+  const bool need_s = mb_s > R.m_s + thr_s;
+  const bool need_t = mb_t > R.m_t + thr_t;
+  if (__any(need_s || need_t)) {
+    const float ns = need_s ? mb_s : R.m_s;
+    const float nt = need_t ? mb_t : R.m_t;
+    const float cs = fast_exp2((R.m_s - ns) * c2s);
+    const float ct = fast_exp2((R.m_t - nt) * c2t);
+    R.m_s = ns;
+    R.m_t = nt;
+    R.nm_s = -ns * c2s;
+    R.nm_t = -nt * c2t;
+    R.l_s *= cs;
+    R.l_t *= ct;
+    R.acc *= ct;
+  }
+}
+
+// Exponentials and sums of one sub-block against the running maxima.
+__device__ __forceinline__ void block_sums(const f32x16& ss, const f32x16& st, SoftRow& R, float c2s, float c2t,
+                                           float ratio) {
+  float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; r += 2) {
+    const float pt0 = fast_exp2(fmaf(st[r], c2t, R.nm_t));
+    const float pt1 = fast_exp2(fmaf(st[r + 1], c2t, R.nm_t));
+    s0 += fast_exp2(fmaf(ss[r], c2s, R.nm_s));
+    s1 += fast_exp2(fmaf(ss[r + 1], c2s, R.nm_s));
+    t0 += pt0;
+    t1 += pt1;
+    a0 = fmaf(pt0, fmaf(st[r], ratio, -ss[r]), a0);
+    a1 = fmaf(pt1, fmaf(st[r + 1], ratio, -ss[r + 1]), a1);
+  }
+  R.l_s += s0 + s1;
+  R.l_t += t0 + t1;
+  R.acc += a0 + a1;
+}
+
 template <int DP, bool BF>
 __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   const RelArgs& a = f.r;
   using TC = TileCopies<DP>;
   constexpr int KS = DP / 16;
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
-  __shared__ __attribute__((aligned(16))) u16 lks[kStages][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[kStages][kTile * DP];
-  __shared__ __attribute__((aligned(16))) unsigned char ltok[kStages][kWaves][kTile];  // one copy per wave
+  // Four tile buffers = two pairs: one pair is consumed while the next lands;
+  // one barrier per pair (4 sub-blocks), so the two waves sharing a SIMD
+  // drift out of phase and overlap MFMA with softmax work between barriers.
+  constexpr int kBufs = 4;
+  __shared__ __attribute__((aligned(16))) u16 lks[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];  // one copy per wave
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches below
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int T = a.T;
@@ -206,6 +299,8 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   const int causal = a.causal;
   const int diag_sb = (row0 >> 5) + w;  // this wave's diagonal 32-key sub-block
 
+  // Negative scales: flip the sign of q (exact) so the effective scale is positive.
+  const u16 flip_s = a.s.scale < 0.f ? 0x8000 : 0, flip_t = a.t.scale < 0.f ? 0x8000 : 0;
   u16x8 fq_s[KS], fq_t[KS];
   {
     const u16* ps = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh + (int64_t)my_i * a.s.q_st;
@@ -214,19 +309,15 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
     for (int kk = 0; kk < KS; ++kk) {
       const int d0 = 16 * kk + 8 * half;
       const bool ld = in_range && d0 < a.s.dim;
-      fq_s[kk] = ld ? *reinterpret_cast<const u16x8*>(ps + d0) : (u16x8)(0);
-      fq_t[kk] = ld ? *reinterpret_cast<const u16x8*>(pt + d0) : (u16x8)(0);
+      fq_s[kk] = ld ? (*reinterpret_cast<const u16x8*>(ps + d0) ^ flip_s) : (u16x8)(0);
+      fq_t[kk] = ld ? (*reinterpret_cast<const u16x8*>(pt + d0) ^ flip_t) : (u16x8)(0);
     }
   }
 
-  const float c2s = a.s.scale2, c2t = a.t.scale2;  // raw logit -> log2 units
-  const float ratio = a.t.scale / a.s.scale;      // x_t - x_s = scale_s * (ratio*st - ss)
+  const float c2s = fabsf(a.s.scale2), c2t = fabsf(a.t.scale2);  // raw logit -> log2 units
+  const float ratio = c2t / c2s;                                 // x_t - x_s = c2s * (ratio*st - ss)
   const float thr_s = kRescaleLog2 / c2s, thr_t = kRescaleLog2 / c2t;
-  // Raw-unit reference maxima; a finite start makes the first valid block
-  // rescale the (zero) sums by exp2(-huge) = 0 without inf - inf.
-  float m_s = -1e30f, m_t = -1e30f;
-  float nm_s = 0.f, nm_t = 0.f;           // -m * c2, refreshed with m
-  float l_s = 0.f, l_t = 0.f, acc = 0.f;  // per-lane partial sums (half of the row's keys)
+  SoftRow R = {kStartMax, kStartMax, -kStartMax * c2s, -kStartMax * c2t, 0.f, 0.f, 0.f};
 
   const int hs = h / a.s.group, ht = h / a.t.group;
   const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
@@ -239,40 +330,20 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   // dominant self-similarity and rescales are rare
   auto tile_of = [&](int it) { return causal ? ntiles - 1 - it : it; };
   auto issue_tile = [&](int it) {
-    const int buf = it % kStages;
+    const int buf = it % kBufs;
     const int j0 = tile_of(it) * kTile;
     issue_rows<DP>(lks[buf], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
     issue_rows<DP>(lkt[buf], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
     issue_small(ltok[buf][w], tok + j0, lane);
   };
-
-  // The register operands loaded above must have landed before the ring
-  // starts: the compiler does not count the asm copies, so a wait it placed
-  // for these loads inside the loop would be vmcnt(0) and drain the ring.
-  wait_vmcnt<0>();
-  issue_tile(0);
-  if (ntiles > 1) issue_tile(1);
-  if (TC::kUniform && ntiles > 1)
-    wait_vmcnt<kPerWave>();
-  else
-    wait_vmcnt<0>();
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it % kStages;
+  auto compute_tile = [&](int it) {
+    const int buf = it % kBufs;
     const int kt0 = tile_of(it) * kTile;
-    const bool more = it + 2 < ntiles;
-    if (more) issue_tile(it + 2);
-    // Tiles with an invalid key take the masked path.  The test reads the
-    // wave's LDS copy of the validity bytes (a global read here would make
-    // the wave drain its copies in flight).
-    const bool col_masked = __any(ltok[buf][w][lane] == 0);
+    const uint64_t tokmask = __ballot(ltok[buf][w][lane] != 0);  // bit j: key kt0 + j valid
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
       if (causal && gsb > diag_sb) continue;
-      const bool masked = col_masked || (causal && gsb == diag_sb);
-
       f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
@@ -280,76 +351,55 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
         ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lks[buf], 32 * sb + l32, c)), fq_s[kk], ss);
         st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lkt[buf], 32 * sb + l32, c)), fq_t[kk], st);
       }
-      if (masked) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int jj = 32 * sb + 8 * (r >> 2) + 4 * half + (r & 3);
-          const bool v = ltok[buf][w][jj] && (!causal || kt0 + jj <= my_i);
-          ss[r] = v ? ss[r] : kNegInf;
-          st[r] = v ? st[r] : kNegInf;
-        }
+      if (tokmask != ~0ull || (causal && gsb == diag_sb)) {
+        const int first = kt0 + 32 * sb + 4 * half;
+        mask_block(ss, st, (unsigned)(tokmask >> (32 * sb + 4 * half)), my_i - first, causal);
       }
-      float mb_s = ss[0], mb_t = st[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) {
-        mb_s = fmaxf(mb_s, ss[r]);
-        mb_t = fmaxf(mb_t, st[r]);
-      }
-      mb_s = fmaxf(mb_s, xor32(mb_s));
-      mb_t = fmaxf(mb_t, xor32(mb_t));
-      const bool need_s = mb_s > m_s + thr_s;
-      const bool need_t = mb_t > m_t + thr_t;
-      if (__any(need_s || need_t)) {
-        const float ns = need_s ? mb_s : m_s;
-        const float nt = need_t ? mb_t : m_t;
-        const float cs = fast_exp2((m_s - ns) * c2s);
-        const float ct = fast_exp2((m_t - nt) * c2t);
-        m_s = ns;
-        m_t = nt;
-        nm_s = -m_s * c2s;
-        nm_t = -m_t * c2t;
-        l_s *= cs;
-        l_t *= ct;
-        acc *= ct;
-      }
-      if (masked) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p_t = fast_exp2(fmaf(st[r], c2t, nm_t));
-          l_s += fast_exp2(fmaf(ss[r], c2s, nm_s));
-          l_t += p_t;
-          acc += (st[r] == kNegInf) ? 0.f : p_t * fmaf(st[r], ratio, -ss[r]);
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p_t = fast_exp2(fmaf(st[r], c2t, nm_t));
-          l_s += fast_exp2(fmaf(ss[r], c2s, nm_s));
-          l_t += p_t;
-          acc = fmaf(p_t, fmaf(st[r], ratio, -ss[r]), acc);
-        }
-      }
+      block_max(ss, st, R, c2s, c2t, thr_s, thr_t);
+      block_sums(ss, st, R, c2s, c2t, ratio);
     }
-    if (TC::kUniform && more)
-      wait_vmcnt<kPerWave>();
-    else
-      wait_vmcnt<0>();
-    __syncthreads();
+  };
+
+  // The register operands loaded above must have landed before the ring
+  // starts: the compiler does not count the asm copies, so a wait it placed
+  // for these loads inside the loop would be vmcnt(0) and drain the ring.
+  wait_vmcnt<0>();
+  for (int it = 0; it < 4 && it < ntiles; ++it) issue_tile(it);
+  if (TC::kUniform && ntiles >= 4)
+    wait_vmcnt<2 * kPerWave>();  // pair 0 landed, pair 1 in flight
+  else if (TC::kUniform && ntiles == 3)
+    wait_vmcnt<kPerWave>();
+  else
+    wait_vmcnt<0>();
+  __syncthreads();
+
+  for (int p = 0; p < ntiles; p += 2) {
+    compute_tile(p);
+    if (p + 1 < ntiles) compute_tile(p + 1);
+    if (p + 2 < ntiles) {
+      wait_vmcnt<0>();  // the next pair (issued one pair ago) landed
+      __syncthreads();  // ... in every wave; this pair's buffers are free
+      if (p + 4 < ntiles) issue_tile(p + 4);
+      if (p + 5 < ntiles) issue_tile(p + 5);
+    }
   }
 
-  l_s += xor32(l_s);
-  l_t += xor32(l_t);
-  acc += xor32(acc);
+  // merge the two halves of the row: common maxima, rescaled sums
+  const float ms = fmaxf(R.m_s, xor32(R.m_s)), mt = fmaxf(R.m_t, xor32(R.m_t));
+  const float fs = fast_exp2((R.m_s - ms) * c2s), ft = fast_exp2((R.m_t - mt) * c2t);
+  const float ls_h = R.l_s * fs, lt_h = R.l_t * ft, acc_h = R.acc * ft;
+  const float l_s = ls_h + xor32(ls_h);
+  const float l_t = lt_h + xor32(lt_h);
+  const float acc = acc_h + xor32(acc_h);
   const bool ok = row_valid && l_s > 0.f && l_t > 0.f;
-  const float ms_nat = m_s * a.s.scale, mt_nat = m_t * a.t.scale;
   const float lg_s = fast_log2(l_s), lg_t = fast_log2(l_t);
+  const float xs = ms * c2s, xt = mt * c2t;  // row maxima, log2 units
   const int64_t row_index = (int64_t)bh * T + my_i;
   if (in_range && half == 0) {
-    f.lse_s_out[row_index] = row_valid ? (l_s > 0.f ? fmaf(lg_s, kLn2, ms_nat) : kNegInf) : 0.f;
-    f.lse_t_out[row_index] = row_valid ? (l_t > 0.f ? fmaf(lg_t, kLn2, mt_nat) : kNegInf) : 0.f;
-    // KL = E_pt[x_t - x_s] + (m_s - m_t) + ln(l_s / l_t)  (natural units); no
-    // two rounded LSEs are subtracted
-    f.row_out[row_index] = ok ? acc * a.s.scale / l_t + (ms_nat - mt_nat) + (lg_s - lg_t) * kLn2 : 0.f;
+    f.lse_s_out[row_index] = row_valid ? (l_s > 0.f ? (xs + lg_s) * kLn2 : kNegInf) : 0.f;
+    f.lse_t_out[row_index] = row_valid ? (l_t > 0.f ? (xt + lg_t) * kLn2 : kNegInf) : 0.f;
+    // KL = E_pt[x_t - x_s] + (max_s - max_t) + ln(l_s / l_t); no two rounded LSEs are subtracted
+    f.row_out[row_index] = ok ? (acc * c2s / l_t + (xs - xt) + (lg_s - lg_t)) * kLn2 : 0.f;
   }
 }
 

@@ -63,7 +63,7 @@ def make_case(B, Hq, Hkv_s, Hkv_t, T, Ds, Dt, dtype, causal, ratio, self_rel, se
         kt = randn((B, Hkv_t, T, Dt), 1.5)
     mask = None
     if ratio is not None:
-        mask = (rng.random((B, T)) > ratio).astype(np.int8)
+        mask = (rng.random((B, T)) > ratio).astype(np.uint8)
         mask[:, 0] = 1
     loss, dq, dk, lse_s, lse_t = O.attn_kl_align(qs, ks, qt, kt, mask, causal, None, None,
                                                  self_relation=False, d_cast=dtype)

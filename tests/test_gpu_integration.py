@@ -188,3 +188,22 @@ def test_hot_path_gqa_masked(gpu_available, causal):
     for got, ref in ((tqs.grad, rdq), (tks.grad, rdk)):
         g = got.float().cpu().numpy()
         assert np.abs(g - ref).max() / np.abs(ref).max() <= 2e-2
+
+
+@pytest.mark.parametrize("a_s,a_t", [(-0.09, -0.09), (0.05, -0.12), (0.3, 0.02)])
+def test_hot_path_signed_and_unequal_scales(gpu_available, a_s, a_t):
+    """Scales of either sign and ratio (the reference accepts any finite scale)."""
+    from linearard_amd.attention_KL import attn_kl_align
+
+    rng = np.random.default_rng(7)
+    B, H, T, D = 1, 2, 333, 128
+    xt = randn(rng, (B, H, T, D), "bf16")
+    xs = O.round_to(xt + 0.3 * rng.standard_normal(xt.shape).astype(np.float32), "bf16")
+    x_s = to_dev(xs, "bf16", requires_grad=True)
+    x_t = to_dev(xt, "bf16")
+    loss = attn_kl_align(x_s, x_s, x_t, x_t, causal=True, sm_scale_s=a_s, sm_scale_t=a_t)
+    loss.backward()
+    rl, rdx, _, _, _ = O.attn_kl_align(xs, xs, xt, xt, None, True, a_s, a_t, self_relation=True)
+    lb = _logit_bound((xs, xs, abs(a_s)), (xt, xt, abs(a_t)))
+    assert _loss_ok(loss.item(), rl, B * H * T, lb), (loss.item(), rl)
+    assert _grad_ok(x_s.grad.float().cpu().numpy(), rdx, xs, abs(a_s), lb)
