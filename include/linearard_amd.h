@@ -119,9 +119,10 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
                          float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
                          void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace needed by lard_attn_kl_backward (bytes): transposed copies of ks
- * and (unless self_relation) qs, one validity byte per token and the two
- * log2-domain row normalisers per query row. */
+/* Workspace needed by lard_attn_kl_backward (bytes): one validity byte per
+ * token and two log2-domain row normalisers per query row.  kv_heads,
+ * head_dim and self_relation do not change the size; they are kept so the
+ * call describes the whole problem. */
 size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,
                                              int64_t head_dim, int self_relation);
 

@@ -163,12 +163,12 @@ int check_blocks(int64_t B, int64_t heads, int64_t T) {
 int64_t padded_len(int64_t T) { return (T + lard::kTile - 1) / lard::kTile * lard::kTile; }
 
 // The throughput kernels address one head of every operand with 32-bit byte
-// offsets: (T-1) * row_stride + D elements and the transposed D * Tp must
-// stay below 2^30 elements.  Larger heads run the stage kernels.
+// offsets: (T-1) * row_stride + D elements must stay below 2^30 elements.
+// Larger heads run the stage kernels.
 bool hot_offsets_ok(std::initializer_list<const lard_tensor4*> ts, int64_t T) {
   constexpr int64_t kMax = (int64_t)1 << 30;
   for (const lard_tensor4* t : ts)
-    if ((T - 1) * t->stride[2] + t->size[3] >= kMax || t->size[3] * padded_len(T) >= kMax) return false;
+    if ((T - 1) * t->stride[2] + t->size[3] >= kMax) return false;
   return true;
 }
 
@@ -224,23 +224,18 @@ FwdWs fwd_layout(void* base, int64_t B, int64_t H, int64_t T, size_t* bytes) {
   return w;
 }
 
-// Backward of the autograd path: transposed keys (and queries unless q is k),
-// token validity, and the log2-domain row normalisers.
+// Backward of the autograd path: token validity and the log2-domain row
+// normalisers (the size depends on B, Hq and T only).
 struct BwdWs {
-  lard::u16* kT;
-  lard::u16* qT;
   unsigned char* tok_ok;
   float* nl_s;
   float* nl_t;
 };
 
-BwdWs bwd_layout(void* base, int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, bool self_relation,
-                 size_t* bytes) {
+BwdWs bwd_layout(void* base, int64_t B, int64_t Hq, int64_t T, size_t* bytes) {
   Carver c(base);
   BwdWs w;
   const int64_t Tp = padded_len(T);
-  w.kT = c.take<lard::u16>(B * Hkv * D * Tp);
-  w.qT = self_relation ? w.kT : c.take<lard::u16>(B * Hq * D * Tp);
   w.tok_ok = c.take<unsigned char>(B * Tp);
   w.nl_s = c.take<float>(B * Hq * Tp);
   w.nl_t = c.take<float>(B * Hq * Tp);
@@ -509,8 +504,11 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
 size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,
                                              int64_t head_dim, int self_relation) {
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  (void)kv_heads;
+  (void)head_dim;
+  (void)self_relation;
   size_t bytes = 0;
-  bwd_layout(nullptr, batch, heads, kv_heads, seq_len, head_dim, self_relation != 0, &bytes);
+  bwd_layout(nullptr, batch, heads, seq_len, &bytes);
   return bytes;
 }
 
@@ -547,18 +545,7 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
       return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
     if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
     const int Tp = (int)padded_len(T);
-    const BwdWs w = bwd_layout(workspace, B, Hq, ks->size[1], T, ds, self_relation != 0, nullptr);
-    if ((rc = hip_status(lard::launch_transpose_keys(static_cast<const lard::u16*>(ks->data), ks->stride[0],
-                                                     ks->stride[1], ks->stride[2], (int)B, (int)ks->size[1], (int)T,
-                                                     ds, Tp, w.kT, st),
-                         "attn_kl_backward transpose launch")) != LARD_OK)
-      return rc;
-    if (!self_relation &&
-        (rc = hip_status(lard::launch_transpose_keys(static_cast<const lard::u16*>(qs->data), qs->stride[0],
-                                                     qs->stride[1], qs->stride[2], (int)B, (int)Hq, (int)T, ds, Tp,
-                                                     w.qT, st),
-                         "attn_kl_backward transpose launch")) != LARD_OK)
-      return rc;
+    const BwdWs w = bwd_layout(workspace, B, Hq, T, nullptr);
     if ((rc = hip_status(lard::launch_token_prep(a, Tp, w.tok_ok, st),
                          "attn_kl_backward token prep launch")) != LARD_OK)
       return rc;
@@ -568,7 +555,6 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
     lard::HotArgs f{};
     f.r = a;
     f.Tp = Tp;
-    f.xT = w.kT;
     f.tok_ok = w.tok_ok;
     f.nl_s = w.nl_s;
     f.nl_t = w.nl_t;
@@ -578,7 +564,6 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
     if ((rc = hip_status(timed(LARD_KERNEL_ROW_GRAD, st, [&] { return lard::launch_hot_dq(f, padded_dim(ds), bf, st); }),
                          "attn_kl_backward dq launch")) != LARD_OK)
       return rc;
-    f.xT = w.qT;
     f.r.dk_out = dk_out;
     f.r.dk_add = self_relation ? dk_out : nullptr;
     f.r.dscale = dloss;

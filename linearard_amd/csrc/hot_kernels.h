@@ -1,12 +1,6 @@
 // Throughput kernels of the autograd path for Ds == Dt <= 128 and one dtype
 // (every shape train.py produces: Llama/Mistral heads are d=128 bf16).
 //
-//   transpose_keys_kernel  x [B,H,T,D] -> xT [B*H][D][Tp] (Tp = T rounded up to
-//                          64, zero padded), keys permuted inside each group of
-//                          16 by sigma = (0-3, 8-11, 4-7, 12-15).  With that
-//                          order the 8 keys a lane needs as the k-slots of the
-//                          second GEMM (accumulator rows 8*(r/4)+4*half+r%4)
-//                          are 16 contiguous bytes, one ds_read_b128.
 //   token_prep_kernel      per token: valid (j < T and mask != 0), one byte.
 //   row_prep_kernel        per query row of the backward: -lse * log2(e) for
 //                          student and teacher, -inf outside the valid set
@@ -18,18 +12,20 @@
 //                          row dq = sm_scale_s D K_s, D = P_s - P_t from the
 //                          forward's LSEs, cast to the input dtype before the
 //                          product exactly like kernel_C.py:232-233, so the
-//                          error is relative to D, not to P.
+//                          error is relative to D, not to P.  The K operand of
+//                          the second GEMM is read transposed from the same
+//                          row-major LDS tile as the first (ds_read_b64_tr_b16).
 //   hot_bwd_kernel         backward, column side (kernel_C.py:242-253): per key
 //                          column dk = sm_scale_s sum_i D_ij q_i, summed over
 //                          the GQA group by its owner (no atomics), plus the
 //                          row side when q is k, times dloss.
 //
 // Memory pipeline: K (fwd, dq) / Q (dk) tiles of 64 rows are copied
-// HBM->LDS with global_load_lds_dwordx4 (no staging registers) into a ring
-// of three LDS buffers: tile t+2 is in flight while tile t is consumed, one
-// barrier per tile.  Every wave issues the same number of copies per tile,
-// so "all but the newest tile landed" is one s_waitcnt vmcnt(N).  LDS tiles
-// are XOR-swizzled by 16-byte chunk so the MFMA operand reads (16 lanes at a
+// HBM->LDS with global_load_lds_dwordx4 (no staging registers) into four LDS
+// buffers used as two tile pairs: one pair is consumed while the next lands,
+// one barrier per pair.  Every wave issues the same number of copies per
+// tile, so "a tile landed" is one s_waitcnt vmcnt(N).  LDS tiles are
+// XOR-swizzled by 16-byte chunk so the MFMA operand reads (16 lanes at a
 // time, one row each) hit 16 distinct bank groups.
 //
 // Work order: workgroups are numbered so that each XCD (8 per MI355X, one L2
@@ -50,7 +46,6 @@ constexpr float kRescaleLog2 = 8.f;  // lazy max: rescale only when the max grow
 
 struct HotArgs {
   RelArgs r;
-  const u16* xT;                 // transposed student keys (dq) / queries (dk): [B*H][D][Tp]
   int Tp;                        // T rounded up to kTile
   const unsigned char* tok_ok;   // [B][Tp] token validity
   const float* nl_s;             // backward: [B*Hq][Tp] -lse_s*log2(e), -inf for excluded rows
@@ -113,21 +108,14 @@ __device__ __forceinline__ const u16* row_chunk(const u16* tile, int r, int c) {
   return tile + (r * CPR + (c ^ (r & (CPR - 1)))) * 8;
 }
 
-// Swizzled transposed tile [DP][kTile]: chunk c (8 keys) of row d at d*8 + (c ^ ((d>>1)&7)).
-__device__ __forceinline__ const u16* tr_chunk(const u16* tile, int d, int c) {
-  return tile + (d * 8 + (c ^ ((d >> 1) & 7))) * 8;
-}
-
 // Copies per wave per tile.  They are uniform across waves when the chunk
 // count of a tile is a multiple of the wave count (D >= 64); otherwise the
 // kernels wait for everything (vmcnt 0) and lose only the look-ahead.
 template <int DP, int NW = kWaves>
 struct TileCopies {
   static constexpr int kRowInst = kTile * (DP / 8) / 64;  // per row tile
-  static constexpr int kTrInst = DP * 8 / 64;             // per transposed tile
   static constexpr bool kUniform = kRowInst % NW == 0;
   static constexpr int kRowPerWave = kRowInst / NW;
-  static constexpr int kTrPerWave = kTrInst / NW;
 };
 
 // Issue the async copy of rows [row0, row0 + kTile) x [0, DP) of one head
@@ -156,31 +144,10 @@ __device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_st
   }
 }
 
-// Issue the async copy of the transposed tile [DP][kTile] starting at key0
-// (srcT = one head of xT, rows Tp apart).  Rows d >= dim copy row 0: they
-// feed output columns that are never stored.
-template <int DP, int NW = kWaves>
-__device__ __forceinline__ void issue_tr(u16* tile, const u16* srcT, int Tp, int key0, int dim, int wave, int lane) {
-  constexpr int NINST = TileCopies<DP>::kTrInst;
-  constexpr int NITER = NINST % NW == 0 ? NINST / NW : (NINST + NW - 1) / NW;
-#pragma unroll
-  for (int i = 0; i < NITER; ++i) {
-    const int n = wave + NW * i;
-    if (NINST % NW != 0 && n >= NINST) break;
-    const int p = 64 * n + lane;
-    const int d = p >> 3;
-    const int c = (p & 7) ^ ((d >> 1) & 7);
-    const int dd = d < dim ? d : 0;
-    lds_async16(srcT, (unsigned)(dd * Tp + key0 + c * 8) * 2u, tile + 64 * n * 8);
-  }
-}
-
 // One copy per wave: 64 bytes (lanes 0-3, 16 each) of `src` into `slot`.
 __device__ __forceinline__ void issue_small(void* slot, const void* src, int lane) {
   if (lane < 4) lds_async16(src, 16u * lane, slot);
 }
-
-__device__ __forceinline__ u16x8 pack8(const u16* v) { return (u16x8){v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]}; }
 
 // ----------------------------------------------------------------------------
 // forward: both online softmaxes and the KL, one pass (2 GEMMs per pair)
@@ -404,25 +371,75 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
 }
 
 // ----------------------------------------------------------------------------
+// backward helpers
+// ----------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// A operand of the second GEMM (m = 32 dims of block db, k-slots = the 16
+// rows 16m..16m+15 of 32-row sub-block sb of a row-major swizzled
+// [kTile][DP] tile), read with two transposing LDS loads
+// (ds_read_b64_tr_b16: in each 16-lane group, lane t receives element t%4 of
+// the 8 bytes that lane 4j + t/4 points at, j = 0..3).  Lane l (group
+// G = l/16, u = l%16) points at row 16m + 8r + 4(G/2) + u/4, dims
+// 32db + 16(G%2) + 4(u%4) .. +3, so lane l receives, for dim 32db + l%32,
+// rows 16m + 8r + 4(l/32) + j: the k-slot order (0-3, 8-11, 4-7, 12-15) of
+// the accumulator registers that D comes from.
+template <int DP>
+__device__ __forceinline__ u16x8 tr_operand(const u16* tile, int sb, int m, int db, int lane) {
+  const int g = lane >> 4, u = lane & 15;
+  int dim = 32 * db + 16 * (g & 1) + 4 * (u & 3);
+  if (DP < 32) dim &= DP - 1;  // lanes whose output dims do not exist read in bounds
+  s16x4 v[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = 32 * sb + 16 * m + 8 * r + 4 * (g >> 1) + (u >> 2);
+    const u16* p = row_chunk<DP>(tile, row, dim >> 3) + (dim & 7);
+    v[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(
+        (__attribute__((address_space(3))) u16*)p));
+  }
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 both = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(u16x8, both);
+}
+
+// B operand of the second GEMM from 8 D values (k-slots in register order),
+// rounded to the input dtype like kernel_C.py:233, two per v_cvt_pk.
+template <bool BF>
+__device__ __forceinline__ u16x8 pack_d(const float* d) {
+  unsigned w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2 x = {d[2 * i], d[2 * i + 1]};
+    if constexpr (BF)
+      w[i] = __builtin_bit_cast(unsigned, __builtin_convertvector(x, bf16x2));
+    else
+      w[i] = __builtin_bit_cast(unsigned, __builtin_convertvector(x, f16x2));
+  }
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(u16x8, (u32x4){w[0], w[1], w[2], w[3]});
+}
+
+// ----------------------------------------------------------------------------
 // backward, row side: dq = sm_scale_s D K_s, one owner per query row
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
 __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   const RelArgs& a = f.r;
   using TC = TileCopies<DP>;
-  constexpr int NT = kWaves * 64;
   constexpr int KS = DP / 16;
-  constexpr int TRR = DP < 32 ? 32 : DP;  // transposed tile rows (>= one 32-wide d block)
-  constexpr int NDB = TRR / 32;
-  constexpr int kPerWave = 2 * TC::kRowPerWave + TC::kTrPerWave + 1;
-  __shared__ __attribute__((aligned(16))) u16 lks[kStages][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[kStages][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkst[kStages][TRR * kTile];
-  __shared__ __attribute__((aligned(16))) unsigned char ltok[kStages][kWaves][kTile];
+  constexpr int NDB = DP >= 32 ? DP / 32 : 1;  // 32-wide dim blocks of dq
+  constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
+  constexpr int kBufs = 4;  // two tile pairs, one barrier per pair
+  __shared__ __attribute__((aligned(16))) u16 lks[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int T = a.T;
@@ -437,13 +454,6 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   const bool in_range = my_i < T;
   const int causal = a.causal;
   const int diag_sb = (row0 >> 5) + w;
-
-  if constexpr (DP < 32) {  // rows DP..31 of the transposed tiles stay zero
-    for (int c = tid; c < kStages * TRR * kTile; c += NT) {
-      const int buf = c / (TRR * kTile), e = c % (TRR * kTile);
-      if (e >= DP * kTile) lkst[buf][e] = 0;
-    }
-  }
 
   u16x8 fq_s[KS], fq_t[KS];
   {
@@ -469,42 +479,24 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   const int hs = h / a.s.group, ht = h / a.t.group;
   const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
   const u16* kt_base = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh;
-  const u16* kst_base = f.xT + ((int64_t)b * a.s.hkv + hs) * a.s.dim * (int64_t)f.Tp;
   const unsigned char* tok = f.tok_ok + (int64_t)b * f.Tp;
 
   const int nkt_all = f.Tp / kTile;
   const int ntiles = causal ? min(nkt_all, (row0 + kRows - 1) / kTile + 1) : nkt_all;
   auto issue_tile = [&](int t) {
-    const int buf = t % kStages;
+    const int buf = t % kBufs;
     const int j0 = t * kTile;
     issue_rows<DP>(lks[buf], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
     issue_rows<DP>(lkt[buf], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
-    issue_tr<DP>(lkst[buf], kst_base, f.Tp, j0, a.s.dim, w, lane);
     issue_small(ltok[buf][w], tok + j0, lane);
   };
-
-  // The register operands loaded above must have landed before the ring
-  // starts: the compiler does not count the asm copies, so a wait it placed
-  // for these loads inside the loop would be vmcnt(0) and drain the ring.
-  wait_vmcnt<0>();
-  issue_tile(0);
-  if (ntiles > 1) issue_tile(1);
-  if (TC::kUniform && ntiles > 1)
-    wait_vmcnt<kPerWave>();
-  else
-    wait_vmcnt<0>();
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t % kStages;
-    const bool more = t + 2 < ntiles;
-    if (more) issue_tile(t + 2);
-    const bool col_masked = __any(ltok[buf][w][lane] == 0);
+  auto compute_tile = [&](int t) {
+    const int buf = t % kBufs;
+    const uint64_t tokmask = __ballot(ltok[buf][w][lane] != 0);  // bit j: key 64t + j valid
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const int gsb = 2 * t + sb;
       if (causal && gsb > diag_sb) continue;
-      const bool masked = col_masked || (causal && gsb == diag_sb);
       f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
@@ -512,30 +504,45 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
         ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lks[buf], 32 * sb + l32, c)), fq_s[kk], ss);
         st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lkt[buf], 32 * sb + l32, c)), fq_t[kk], st);
       }
-      u16 dv[16];
+      float dd[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float dd = fast_exp2(fmaf(ss[r], c2s, nls2)) - fast_exp2(fmaf(st[r], c2t, nlt2));
-        if (masked) {
-          const int jj = 32 * sb + 8 * (r >> 2) + 4 * half + (r & 3);
-          dd = (ltok[buf][w][jj] && (!causal || t * kTile + jj <= my_i)) ? dd : 0.f;
+      for (int r = 0; r < 16; ++r) dd[r] = fast_exp2(fmaf(ss[r], c2s, nls2)) - fast_exp2(fmaf(st[r], c2t, nlt2));
+      if (tokmask != ~0ull || (causal && gsb == diag_sb)) {
+        const unsigned bits = (unsigned)(tokmask >> (32 * sb + 4 * half));
+        const int lim = my_i - (t * kTile + 32 * sb + 4 * half);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int off = 8 * (r >> 2) + (r & 3);
+          dd[r] = (((bits >> off) & 1u) && (!causal || off <= lim)) ? dd[r] : 0.f;
         }
-        dv[r] = to_bits(dd, BF);  // D cast to the input dtype (kernel_C.py:233)
       }
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const u16x8 bop = pack8(dv + 8 * m);
-        const int c = 2 * (2 * sb + m) + half;  // 8-key chunk of the permuted tile
+        const u16x8 bop = pack_d<BF>(dd + 8 * m);  // D cast to the input dtype (kernel_C.py:233)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          dq[db] = mfma32<BF>(*reinterpret_cast<const u16x8*>(tr_chunk(lkst[buf], 32 * db + l32, c)), bop, dq[db]);
+        for (int db = 0; db < NDB; ++db) dq[db] = mfma32<BF>(tr_operand<DP>(lks[buf], sb, m, db, lane), bop, dq[db]);
       }
     }
-    if (TC::kUniform && more)
-      wait_vmcnt<kPerWave>();
-    else
+  };
+
+  wait_vmcnt<0>();  // register operands landed before the ring starts
+  for (int t = 0; t < 4 && t < ntiles; ++t) issue_tile(t);
+  if (TC::kUniform && ntiles >= 4)
+    wait_vmcnt<2 * kPerWave>();
+  else if (TC::kUniform && ntiles == 3)
+    wait_vmcnt<kPerWave>();
+  else
+    wait_vmcnt<0>();
+  __syncthreads();
+  for (int p = 0; p < ntiles; p += 2) {
+    compute_tile(p);
+    if (p + 1 < ntiles) compute_tile(p + 1);
+    if (p + 2 < ntiles) {
       wait_vmcnt<0>();
-    __syncthreads();
+      __syncthreads();
+      if (p + 4 < ntiles) issue_tile(p + 4);
+      if (p + 5 < ntiles) issue_tile(p + 5);
+    }
   }
 
   if (in_range) {
@@ -559,24 +566,22 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
 // backward, column side: dk = sm_scale_s sum_{h in group} D^T Q_s
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
-__global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f) {
+__global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
   const RelArgs& a = f.r;
   using TC = TileCopies<DP>;
-  constexpr int NT = kWaves * 64;
   constexpr int KS = DP / 16;
-  constexpr int TRR = DP < 32 ? 32 : DP;
-  constexpr int NDB = TRR / 32;
-  constexpr int kPerWave = 2 * TC::kRowPerWave + TC::kTrPerWave + 1;
-  __shared__ __attribute__((aligned(16))) u16 lqs[kStages][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lqt[kStages][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lqst[kStages][TRR * kTile];
+  constexpr int NDB = DP >= 32 ? DP / 32 : 1;
+  constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
+  constexpr int kBufs = 4;
+  __shared__ __attribute__((aligned(16))) u16 lqs[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lqt[kBufs][kTile * DP];
   // per query row of the tile: -lse*log2(e) of student [0, 64) and teacher [64, 128)
-  __shared__ __attribute__((aligned(16))) float lnl[kStages][2 * kTile];
+  __shared__ __attribute__((aligned(16))) float lnl[kBufs][2 * kTile];
   static_assert(2 * kTile * sizeof(float) == kWaves * 64, "one 64-byte row-data copy per wave");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int T = a.T;
@@ -592,13 +597,6 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
   const bool col_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_j);
   const int causal = a.causal;
   const int diag_sb = j0w >> 5;  // the 32-row sub-block holding this wave's diagonal
-
-  if constexpr (DP < 32) {
-    for (int c = tid; c < kStages * TRR * kTile; c += NT) {
-      const int buf = c / (TRR * kTile), e = c % (TRR * kTile);
-      if (e >= DP * kTile) lqst[buf][e] = 0;
-    }
-  }
 
   u16x8 fk_s[KS], fk_t[KS];
   {
@@ -637,38 +635,23 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
     const int64_t bh = (int64_t)b * a.Hq + h;
     const u16* qs_base = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh;
     const u16* qt_base = a.t.q + (int64_t)b * a.t.q_sb + (int64_t)h * a.t.q_sh;
-    const u16* qst_base = f.xT + bh * a.s.dim * (int64_t)f.Tp;
     // wave w copies 16 normalisers: student rows 16w.. (w < 4), teacher rows 16(w-4).. (w >= 4)
     const float* nl_src = (w < 4 ? f.nl_s : f.nl_t) + bh * f.Tp + 16 * (w & 3);
 
     auto issue_tile = [&](int it) {
-      const int buf = it % kStages;
+      const int buf = it % kBufs;
       const int i0 = tile_of(it) * kTile;
       issue_rows<DP>(lqs[buf], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
       issue_rows<DP>(lqt[buf], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
-      issue_tr<DP>(lqst[buf], qst_base, f.Tp, i0, a.s.dim, w, lane);
       issue_small(&lnl[buf][16 * w], nl_src + i0, lane);
     };
-
-    wait_vmcnt<0>();  // teacher key fragments landed before the ring starts
-    issue_tile(0);
-    if (ntiles > 1) issue_tile(1);
-    if (TC::kUniform && ntiles > 1)
-      wait_vmcnt<kPerWave>();
-    else
-      wait_vmcnt<0>();
-    __syncthreads();
-
-    for (int it = 0; it < ntiles; ++it) {
-      const int buf = it % kStages;
+    auto compute_tile = [&](int it) {
+      const int buf = it % kBufs;
       const int t = tile_of(it);
-      const bool more = it + 2 < ntiles;
-      if (more) issue_tile(it + 2);
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int gsb = 2 * t + sb;
         if (causal && gsb < diag_sb) continue;
-        const bool diag = causal && gsb == diag_sb;
         f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
@@ -676,35 +659,54 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
           ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lqs[buf], 32 * sb + l32, c)), fk_s[kk], ss);
           st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lqt[buf], 32 * sb + l32, c)), fk_t[kk], st);
         }
-        u16 dv[16];
+        float dd[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int ii0 = 32 * sb + 8 * r4 + 4 * half;
           const f32x4 ls4 = *reinterpret_cast<const f32x4*>(&lnl[buf][ii0]);
           const f32x4 lt4 = *reinterpret_cast<const f32x4*>(&lnl[buf][kTile + ii0]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * r4 + e;
-            float dd = fast_exp2(fmaf(ss[r], c2s, ls4[e])) - fast_exp2(fmaf(st[r], c2t, lt4[e]));
-            if (diag) dd = (t * kTile + ii0 + e >= my_j) ? dd : 0.f;
-            dv[r] = to_bits(dd, BF);  // D cast to the input dtype (kernel_C.py:233)
+          for (int e = 0; e < 4; ++e)
+            dd[4 * r4 + e] = fast_exp2(fmaf(ss[4 * r4 + e], c2s, ls4[e])) - fast_exp2(fmaf(st[4 * r4 + e], c2t, lt4[e]));
+        }
+        if (causal && gsb == diag_sb) {
+          const int lim = t * kTile + 32 * sb + 4 * half - my_j;  // row(r) - column = off(r) + lim
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 8 * (r >> 2) + (r & 3);
+            dd[r] = off + lim >= 0 ? dd[r] : 0.f;
           }
         }
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-          const u16x8 bop = pack8(dv + 8 * m);
-          const int c = 2 * (2 * sb + m) + half;
+          const u16x8 bop = pack_d<BF>(dd + 8 * m);  // D cast to the input dtype (kernel_C.py:233)
 #pragma unroll
           for (int db = 0; db < NDB; ++db)
-            dk[db] = mfma32<BF>(*reinterpret_cast<const u16x8*>(tr_chunk(lqst[buf], 32 * db + l32, c)), bop, dk[db]);
+            dk[db] = mfma32<BF>(tr_operand<DP>(lqs[buf], sb, m, db, lane), bop, dk[db]);
         }
       }
-      if (TC::kUniform && more)
-        wait_vmcnt<kPerWave>();
-      else
+    };
+
+    wait_vmcnt<0>();  // register operands landed before the ring starts
+    for (int it = 0; it < 4 && it < ntiles; ++it) issue_tile(it);
+    if (TC::kUniform && ntiles >= 4)
+      wait_vmcnt<2 * kPerWave>();
+    else if (TC::kUniform && ntiles == 3)
+      wait_vmcnt<kPerWave>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    for (int p = 0; p < ntiles; p += 2) {
+      compute_tile(p);
+      if (p + 1 < ntiles) compute_tile(p + 1);
+      if (p + 2 < ntiles) {
         wait_vmcnt<0>();
-      __syncthreads();
+        __syncthreads();
+        if (p + 4 < ntiles) issue_tile(p + 4);
+        if (p + 5 < ntiles) issue_tile(p + 5);
+      }
     }
+    __syncthreads();  // every wave is done with the ring before the next head refills it
   }
 
   if (in_range) {
@@ -729,13 +731,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void hot_bwd_kernel(const HotArgs f
   }
 }
 
-// Transposed, key-permuted copy of x for the second GEMM of both backward kernels.
-__global__ void transpose_keys_kernel(const u16* __restrict__ x, int64_t sb, int64_t sh, int64_t st, int H, int T,
-                                      int D, int Tp, u16* __restrict__ xT);
-
 bool hot_supported(int ds, int dt, bool same_dtype);
-hipError_t launch_transpose_keys(const u16* x, int64_t sb, int64_t sh, int64_t st, int B, int H, int T, int D, int Tp,
-                                 u16* xT, hipStream_t stream);
 hipError_t launch_token_prep(const RelArgs& a, int Tp, unsigned char* tok_ok, hipStream_t stream);
 hipError_t launch_row_prep(const RelArgs& a, int Tp, const unsigned char* tok_ok, float* nl_s, float* nl_t,
                            hipStream_t stream);

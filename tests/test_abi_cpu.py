@@ -61,13 +61,12 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert L.lard_kl_forward_workspace_bytes(0, 3, 5) == 0
     # forward of the autograd path adds one validity byte per (padded) token
     assert L.lard_attn_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8 + 4 * 4096
-    # backward: transposed keys (+ queries unless q is k), validity, 2 normalisers per row
+    # backward: validity bytes and 2 normalisers per (padded) row
     B, H, T, D = 2, 8, 1000, 64
     Tp = 1024
-    kt = B * H * D * Tp * 2
     tail = B * Tp + 2 * B * H * Tp * 4
-    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 1) == kt + tail
-    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 0) == 2 * kt + tail
+    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 1) == tail
+    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 0) == tail
     assert L.lard_attn_kl_backward_workspace_bytes(0, H, H, T, D, 0) == 0
 
 
