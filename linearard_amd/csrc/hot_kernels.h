@@ -101,11 +101,24 @@ __device__ __forceinline__ int xcd_item(int bid, int n) {
 }
 
 // Swizzled row tile [kTile][DP]: chunk c (8 elements) of row r is stored at
-// chunk index r*CPR + (c ^ (r & (CPR-1))).
+// chunk slot r*CPR + (c ^ swz(r)).  The read patterns that must be free of
+// bank conflicts (64 banks x 4 bytes): 16 consecutive rows at one chunk (the
+// 16-byte operand reads), and for the transposing reads of the backward,
+// aligned blocks of 4 rows x 4 chunks.  For D = 128, swz(r) = 4(r%4) +
+// 2((r/4)%2) + (r/8)%2 is a bijection on 16 consecutive rows and sends such
+// a block to 16 distinct slots (the plain r%16 sends it to 4 slots).
+template <int DP>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (DP == 128)
+    return 4 * (r & 3) + 2 * ((r >> 2) & 1) + ((r >> 3) & 1);
+  else
+    return r & (DP / 8 - 1);
+}
+
 template <int DP>
 __device__ __forceinline__ const u16* row_chunk(const u16* tile, int r, int c) {
   constexpr int CPR = DP / 8;
-  return tile + (r * CPR + (c ^ (r & (CPR - 1)))) * 8;
+  return tile + (r * CPR + (c ^ swz<DP>(r))) * 8;
 }
 
 // Copies per wave per tile.  They are uniform across waves when the chunk
@@ -137,7 +150,7 @@ __device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_st
     if (NINST % NW != 0 && n >= NINST) break;
     const int p = 64 * n + lane;
     const int r = p / CPR;
-    int c = (p % CPR) ^ (r & (CPR - 1));
+    int c = (p % CPR) ^ swz<DP>(r);  // logical chunk stored at this slot (XOR is an involution)
     c = c * 8 < dim ? c : 0;
     const int row = min(row0 + r, T - 1);
     lds_async16(src, (unsigned)(row * row_stride + c * 8) * 2u, tile + 64 * n * 8);
