@@ -42,7 +42,6 @@ constexpr int kWaves = 8;     // waves per workgroup: 8 x 32 rows / columns
 constexpr int kRows = kWaves * 32;
 constexpr int kStages = 3;    // LDS ring depth
 constexpr int kXcds = 8;
-constexpr float kRescaleLog2 = 8.f;  // lazy max: rescale only when the max grows by > 2^8
 
 struct HotArgs {
   RelArgs r;
@@ -168,8 +167,8 @@ __device__ __forceinline__ void issue_small(void* slot, const void* src, int lan
 // Softmax state: each lane keeps its own running maxima for its half of the
 // row's keys (lanes l and l+32 share a row), so the loop needs no cross-lane
 // exchange; the halves are merged once at the end.  The maxima are lazy (a
-// rescale only when a block max exceeds the running max by 2^8 in
-// probability), in raw logit units; a negative scale is handled by flipping
+// rescale only when a sub-block's sums exceed 2^8, see add_block), in raw
+// logit units; a negative scale is handled by flipping
 // the sign of q (exact), so the effective scale is positive.  Masked elements
 // (causal diagonal, invalid keys) are set to -1e30 in place: with running
 // maxima starting at -5e29 their exponentials are exactly 0 and every product
@@ -199,36 +198,13 @@ __device__ __forceinline__ void mask_block(f32x16& ss, f32x16& st, unsigned bits
   }
 }
 
-// Lazy max update: rescale the lane's sums when a block max exceeds the
-// running max by more than `thr` (raw units); uniform branch, rare.
-__device__ __forceinline__ void block_max(const f32x16& ss, const f32x16& st, SoftRow& R, float c2s, float c2t,
-                                          float thr_s, float thr_t) {
-  float mb_s = fmaxf(ss[0], ss[1]), mb_t = fmaxf(st[0], st[1]);
-#pragma unroll
-  for (int r = 2; r < 16; r += 2) {
-    mb_s = fmaxf(fmaxf(mb_s, ss[r]), ss[r + 1]);
-    mb_t = fmaxf(fmaxf(mb_t, st[r]), st[r + 1]);
-  }
-  const bool need_s = mb_s > R.m_s + thr_s;
-  const bool need_t = mb_t > R.m_t + thr_t;
-  if (__any(need_s || need_t)) {
-    const float ns = need_s ? mb_s : R.m_s;
-    const float nt = need_t ? mb_t : R.m_t;
-    const float cs = fast_exp2((R.m_s - ns) * c2s);
-    const float ct = fast_exp2((R.m_t - nt) * c2t);
-    R.m_s = ns;
-    R.m_t = nt;
-    R.nm_s = -ns * c2s;
-    R.nm_t = -nt * c2t;
-    R.l_s *= cs;
-    R.l_t *= ct;
-    R.acc *= ct;
-  }
-}
+// Partial sums of one sub-block against the running maxima.
+struct BlockSums {
+  float s, t, a;  // sum p_s, sum p_t, sum p_t * (ratio * st - ss)   (unnormalised)
+};
 
-// Exponentials and sums of one sub-block against the running maxima.
-__device__ __forceinline__ void block_sums(const f32x16& ss, const f32x16& st, SoftRow& R, float c2s, float c2t,
-                                           float ratio) {
+__device__ __forceinline__ BlockSums block_sums(const f32x16& ss, const f32x16& st, const SoftRow& R, float c2s,
+                                                float c2t, float ratio) {
   float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; r += 2) {
@@ -241,9 +217,114 @@ __device__ __forceinline__ void block_sums(const f32x16& ss, const f32x16& st, S
     a0 = fmaf(pt0, fmaf(st[r], ratio, -ss[r]), a0);
     a1 = fmaf(pt1, fmaf(st[r + 1], ratio, -ss[r + 1]), a1);
   }
-  R.l_s += s0 + s1;
-  R.l_t += t0 + t1;
-  R.acc += a0 + a1;
+  return {s0 + s1, t0 + t1, a0 + a1};
+}
+
+// Raise the running maxima to the sub-block's maxima where those are larger,
+// rescaling the sums.
+__device__ __forceinline__ void raise_max(const f32x16& ss, const f32x16& st, SoftRow& R, float c2s, float c2t) {
+  float mb_s = fmaxf(ss[0], ss[1]), mb_t = fmaxf(st[0], st[1]);
+#pragma unroll
+  for (int r = 2; r < 16; r += 2) {
+    mb_s = fmaxf(fmaxf(mb_s, ss[r]), ss[r + 1]);
+    mb_t = fmaxf(fmaxf(mb_t, st[r]), st[r + 1]);
+  }
+  const float ns = fmaxf(mb_s, R.m_s), nt = fmaxf(mb_t, R.m_t);
+  const float cs = fast_exp2((R.m_s - ns) * c2s);
+  const float ct = fast_exp2((R.m_t - nt) * c2t);
+  R.m_s = ns;
+  R.m_t = nt;
+  R.nm_s = -ns * c2s;
+  R.nm_t = -nt * c2t;
+  R.l_s *= cs;
+  R.l_t *= ct;
+  R.acc *= ct;
+}
+
+// Lazy maxima, checked on the sums: a lane's sub-block sums stay below
+// kLazySum (so every exponential is below it) unless a logit exceeds the
+// running max by more than log2(kLazySum) = 20 in log2 units, or the running
+// max is still kStartMax (the sums are then +inf).  Only then (a uniform,
+// rare branch: in practice the first valid sub-block of a row) are the
+// maxima raised and the sub-block recomputed.  Sums kept this way stay below
+// 2^20 * T < 2^52: no overflow, and fp32 relative precision throughout (the
+// exponentials below the running max lose nothing they would not lose
+// against the true max, which is at most 2^20 larger).
+constexpr float kLazySum = 1048576.f;  // 2^20
+
+__device__ __forceinline__ void add_block(const f32x16& ss, const f32x16& st, BlockSums bs, SoftRow& R, float c2s,
+                                          float c2t, float ratio) {
+  if (__any(!(bs.s <= kLazySum) || !(bs.t <= kLazySum))) {
+    raise_max(ss, st, R, c2s, c2t);
+    bs = block_sums(ss, st, R, c2s, c2t, ratio);
+  }
+  R.l_s += bs.s;
+  R.l_t += bs.t;
+  R.acc += bs.a;
+}
+
+// S = K Q^T for one 32-key sub-block (rows r0.. of the swizzled student LDS
+// tile ks; the teacher tile follows it), both relations: 2 x DP/16 MFMAs.
+template <int DP, bool BF>
+__device__ __forceinline__ void sub_scores(const u16* ks, int r0, int l32, int half, const u16x8* fq_s,
+                                           const u16x8* fq_t, f32x16& ss, f32x16& st) {
+  ss = (f32x16)(0.f);
+  st = (f32x16)(0.f);
+#pragma unroll
+  for (int kk = 0; kk < DP / 16; ++kk) {
+    const u16* p = row_chunk<DP>(ks, r0 + l32, 2 * kk + half);
+    ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(p), fq_s[kk], ss);
+    st = mfma32<BF>(*reinterpret_cast<const u16x8*>(p + kTile * DP), fq_t[kk], st);
+  }
+}
+
+// One pipeline step of the forward: the scores of the next sub-block
+// (ns, nt; LDS row `row` of the student tile `ks`, whose teacher tile
+// follows it) and the softmax sums of the current one (ss, st),
+// interleaved by hand: each k-step's two MFMAs are followed by the VALU work
+// of 16/KS of the current sub-block's elements, and scheduling barriers keep
+// that order, so the matrix unit and the VALU work at the same time within
+// the wave.  LDS operands are read PD k-steps ahead.
+template <int DP, bool BF, int PD = 2>
+__device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int half,
+                                                     const u16x8* fq_s, const u16x8* fq_t, f32x16& ns, f32x16& nt,
+                                                     const f32x16& ss, const f32x16& st, const SoftRow& R, float c2s,
+                                                     float c2t, float ratio) {
+  constexpr int KS = DP / 16, EP = 16 / KS;
+  u16x8 os[KS], ot[KS];
+  auto load = [&](int kk) {
+    const u16* p = row_chunk<DP>(ks, row, 2 * kk + half);
+    os[kk] = *reinterpret_cast<const u16x8*>(p);
+    ot[kk] = *reinterpret_cast<const u16x8*>(p + kTile * DP);  // same slot of the teacher tile
+  };
+#pragma unroll
+  for (int kk = 0; kk < PD && kk < KS; ++kk) load(kk);
+  ns = (f32x16)(0.f);
+  nt = (f32x16)(0.f);
+  float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    if (kk + PD < KS) load(kk + PD);
+    ns = mfma32<BF>(os[kk], fq_s[kk], ns);
+    nt = mfma32<BF>(ot[kk], fq_t[kk], nt);
+#pragma unroll
+    for (int e = 0; e < EP; e += 2) {
+      const int r = kk * EP + e;
+      const float pt0 = fast_exp2(fmaf(st[r], c2t, R.nm_t));
+      const float pt1 = fast_exp2(fmaf(st[r + 1], c2t, R.nm_t));
+      s0 += fast_exp2(fmaf(ss[r], c2s, R.nm_s));
+      s1 += fast_exp2(fmaf(ss[r + 1], c2s, R.nm_s));
+      t0 += pt0;
+      t1 += pt1;
+      a0 = fmaf(pt0, fmaf(st[r], ratio, -ss[r]), a0);
+      a1 = fmaf(pt1, fmaf(st[r + 1], ratio, -ss[r + 1]), a1);
+    }
+    // the empty asm consumes this k-step's sums, so no IR pass can sink their
+    // arithmetic past the scheduling barrier
+    asm volatile("" : "+v"(s0), "+v"(s1), "+v"(t0), "+v"(t1), "+v"(a0), "+v"(a1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return {s0 + s1, t0 + t1, a0 + a1};
 }
 
 template <int DP, bool BF>
@@ -253,11 +334,9 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   constexpr int KS = DP / 16;
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
   // Four tile buffers = two pairs: one pair is consumed while the next lands;
-  // one barrier per pair (4 sub-blocks), so the two waves sharing a SIMD
-  // drift out of phase and overlap MFMA with softmax work between barriers.
+  // one barrier per pair (4 sub-blocks).
   constexpr int kBufs = 4;
-  __shared__ __attribute__((aligned(16))) u16 lks[kBufs][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];  // one copy per wave
 
   const int tid = threadIdx.x;
@@ -296,7 +375,6 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
 
   const float c2s = fabsf(a.s.scale2), c2t = fabsf(a.t.scale2);  // raw logit -> log2 units
   const float ratio = c2t / c2s;                                 // x_t - x_s = c2s * (ratio*st - ss)
-  const float thr_s = kRescaleLog2 / c2s, thr_t = kRescaleLog2 / c2t;
   SoftRow R = {kStartMax, kStartMax, -kStartMax * c2s, -kStartMax * c2t, 0.f, 0.f, 0.f};
 
   const int hs = h / a.s.group, ht = h / a.t.group;
@@ -312,32 +390,45 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   auto issue_tile = [&](int it) {
     const int buf = it % kBufs;
     const int j0 = tile_of(it) * kTile;
-    issue_rows<DP>(lks[buf], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
-    issue_rows<DP>(lkt[buf], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    issue_rows<DP>(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+    issue_rows<DP>(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
     issue_small(ltok[buf][w], tok + j0, lane);
   };
-  auto compute_tile = [&](int it) {
+
+  // Software pipeline over 32-key sub-blocks k = 2*tile + sb: the scores of
+  // sub-block k+1 are computed while the softmax sums of sub-block k run.
+  // Sub-blocks above the causal diagonal are not skipped but fully masked:
+  // every wave then runs the same straight-line steps, and the wave holding
+  // the last rows (which has no such sub-block) sets the pace anyway.
+  struct Sub {
+    f32x16 s, t;
+    uint64_t tm;  // token validity of its tile, bit j = key j of the tile
+  };
+  auto scores = [&](Sub& x, int it, int sb) {
     const int buf = it % kBufs;
+    x.tm = __ballot(ltok[buf][w][lane] != 0);  // read now: the buffer is refilled before its softmax
+    sub_scores<DP, BF>(lk[buf][0], 32 * sb, l32, half, fq_s, fq_t, x.s, x.t);
+  };
+  auto prepare = [&](Sub& x, int it, int sb) {
     const int kt0 = tile_of(it) * kTile;
-    const uint64_t tokmask = __ballot(ltok[buf][w][lane] != 0);  // bit j: key kt0 + j valid
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
-      if (causal && gsb > diag_sb) continue;
-      f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const int c = 2 * kk + half;
-        ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lks[buf], 32 * sb + l32, c)), fq_s[kk], ss);
-        st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lkt[buf], 32 * sb + l32, c)), fq_t[kk], st);
-      }
-      if (tokmask != ~0ull || (causal && gsb == diag_sb)) {
-        const int first = kt0 + 32 * sb + 4 * half;
-        mask_block(ss, st, (unsigned)(tokmask >> (32 * sb + 4 * half)), my_i - first, causal);
-      }
-      block_max(ss, st, R, c2s, c2t, thr_s, thr_t);
-      block_sums(ss, st, R, c2s, c2t, ratio);
+    const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
+    if (x.tm != ~0ull || (causal && gsb >= diag_sb)) {
+      const int first = kt0 + 32 * sb + 4 * half;
+      mask_block(x.s, x.t, (unsigned)(x.tm >> (32 * sb + 4 * half)), my_i - first, causal);
     }
+  };
+  // softmax of cur (tile it, half sb) while the scores of nxt (tile it2, half sb2) run
+  auto step = [&](Sub& cur, int it, int sb, Sub& nxt, int it2, int sb2) {
+    prepare(cur, it, sb);
+    const int buf = it2 % kBufs;
+    nxt.tm = __ballot(ltok[buf][w][lane] != 0);  // read now: the buffer is refilled before its softmax
+    const BlockSums bs = scores_and_sums<DP, BF>(lk[buf][0], 32 * sb2 + l32, half, fq_s, fq_t, nxt.s,
+                                                 nxt.t, cur.s, cur.t, R, c2s, c2t, ratio);
+    add_block(cur.s, cur.t, bs, R, c2s, c2t, ratio);
+  };
+  auto last = [&](Sub& cur, int it, int sb) {
+    prepare(cur, it, sb);
+    add_block(cur.s, cur.t, block_sums(cur.s, cur.t, R, c2s, c2t, ratio), R, c2s, c2t, ratio);
   };
 
   // The register operands loaded above must have landed before the ring
@@ -353,15 +444,24 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
     wait_vmcnt<0>();
   __syncthreads();
 
-  for (int p = 0; p < ntiles; p += 2) {
-    compute_tile(p);
-    if (p + 1 < ntiles) compute_tile(p + 1);
-    if (p + 2 < ntiles) {
-      wait_vmcnt<0>();  // the next pair (issued one pair ago) landed
-      __syncthreads();  // ... in every wave; this pair's buffers are free
-      if (p + 4 < ntiles) issue_tile(p + 4);
-      if (p + 5 < ntiles) issue_tile(p + 5);
+  // sub-block k = 2 * tile + half; A holds the even ones, B the odd ones
+  const int nsub = 2 * ntiles;
+  Sub A, B;
+  scores(A, 0, 0);
+  for (int k = 0;; k += 2) {
+    step(A, k >> 1, 0, B, k >> 1, 1);
+    if (k + 2 >= nsub) {
+      last(B, k >> 1, 1);
+      break;
     }
+    if ((k & 3) == 2) {  // sub-block k + 2 starts the next tile pair
+      wait_vmcnt<0>();   // which landed (it was issued one pair ago)
+      __syncthreads();   // ... in every wave; this pair's buffers are free
+      const int p4 = (k >> 1) + 3;
+      if (p4 < ntiles) issue_tile(p4);
+      if (p4 + 1 < ntiles) issue_tile(p4 + 1);
+    }
+    step(B, k >> 1, 1, A, (k >> 1) + 1, 0);
   }
 
   // merge the two halves of the row: common maxima, rescaled sums
