@@ -115,9 +115,14 @@ __device__ __forceinline__ int swz(int r) {
 }
 
 template <int DP>
-__device__ __forceinline__ const u16* row_chunk(const u16* tile, int r, int c) {
+__device__ __forceinline__ int row_chunk_off(int r, int c) {  // u16 elements
   constexpr int CPR = DP / 8;
-  return tile + (r * CPR + (c ^ swz<DP>(r))) * 8;
+  return (r * CPR + (c ^ swz<DP>(r))) * 8;
+}
+
+template <int DP>
+__device__ __forceinline__ const u16* row_chunk(const u16* tile, int r, int c) {
+  return tile + row_chunk_off<DP>(r, c);
 }
 
 // Copies per wave per tile.  They are uniform across waves when the chunk
@@ -155,6 +160,41 @@ __device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_st
     lds_async16(src, (unsigned)(row * row_stride + c * 8) * 2u, tile + 64 * n * 8);
   }
 }
+
+// issue_rows with the per-lane byte offsets of a full tile computed once:
+// a full tile then costs one uniform base pointer and the copies; the last,
+// partial tile (rows clamped to T - 1) goes through issue_rows.
+template <int DP, int NW = kWaves>
+struct RowCopier {
+  static constexpr int CPR = DP / 8;
+  static constexpr int NINST = TileCopies<DP, NW>::kRowInst;
+  static constexpr int NITER = NINST % NW == 0 ? NINST / NW : (NINST + NW - 1) / NW;
+  unsigned voff[NITER];
+  __device__ __forceinline__ void init(int row_stride, int dim, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < NITER; ++i) {
+      const int p = 64 * (wave + NW * i) + lane;
+      const int r = p / CPR;
+      int c = (p % CPR) ^ swz<DP>(r);
+      c = c * 8 < dim ? c : 0;
+      voff[i] = (unsigned)(r * row_stride + c * 8) * 2u;
+    }
+  }
+  __device__ __forceinline__ void issue(u16* tile, const u16* src, int row_stride, int row0, int T, int dim, int wave,
+                                        int lane) const {
+    if (row0 + kTile <= T) {
+      const u16* base = src + (int64_t)row0 * row_stride;
+#pragma unroll
+      for (int i = 0; i < NITER; ++i) {
+        const int n = wave + NW * i;
+        if (NINST % NW != 0 && n >= NINST) break;
+        lds_async16(base, voff[i], tile + 64 * n * 8);
+      }
+    } else {
+      issue_rows<DP, NW>(tile, src, row_stride, row0, T, dim, wave, lane);
+    }
+  }
+};
 
 // One copy per wave: 64 bytes (lanes 0-3, 16 each) of `src` into `slot`.
 __device__ __forceinline__ void issue_small(void* slot, const void* src, int lane) {
@@ -387,11 +427,14 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   // causal: the diagonal tiles first, so the running max is set by the
   // dominant self-similarity and rescales are rare
   auto tile_of = [&](int it) { return causal ? ntiles - 1 - it : it; };
+  RowCopier<DP> cp_s, cp_t;
+  cp_s.init((int)a.s.k_st, a.s.dim, w, lane);
+  cp_t.init((int)a.t.k_st, a.t.dim, w, lane);
   auto issue_tile = [&](int it) {
     const int buf = it % kBufs;
     const int j0 = tile_of(it) * kTile;
-    issue_rows<DP>(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
-    issue_rows<DP>(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    cp_s.issue(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+    cp_t.issue(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
     issue_small(ltok[buf][w], tok + j0, lane);
   };
 
@@ -518,6 +561,39 @@ __device__ __forceinline__ u16x8 tr_operand(const u16* tile, int sb, int m, int 
   return __builtin_bit_cast(u16x8, both);
 }
 
+// tr_operand with the per-lane offsets computed once: the operand of rows
+// 32sb + 16m .. and dims 32db .. is the tile base + a compile-time row offset
+// + off[r][db].
+template <int DP>
+struct TrOffsets {
+  static constexpr int NDB = DP >= 32 ? DP / 32 : 1;
+  unsigned off[2][NDB];  // u16 elements
+  __device__ __forceinline__ void init(int lane) {
+    const int g = lane >> 4, u = lane & 15;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      int dim = 32 * db + 16 * (g & 1) + 4 * (u & 3);
+      if (DP < 32) dim &= DP - 1;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = 8 * r + 4 * (g >> 1) + (u >> 2);  // < 16: the swizzle of rows 16j + row is that of row
+        off[r][db] = (unsigned)row_chunk_off<DP>(row, dim >> 3) + (dim & 7);
+      }
+    }
+  }
+  __device__ __forceinline__ u16x8 read(const u16* tile, int sb, int m, int db) const {
+    const u16* base = tile + (32 * sb + 16 * m) * DP;
+    s16x4 v[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      v[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)((__attribute__((address_space(3))) u16*)(base + off[r][db])));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 both = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(u16x8, both);
+  }
+};
+
 // B operand of the second GEMM from 8 D values (k-slots in register order),
 // rounded to the input dtype like kernel_C.py:233, two per v_cvt_pk.
 template <bool BF>
@@ -536,6 +612,102 @@ __device__ __forceinline__ u16x8 pack_d(const float* d) {
 }
 
 // ----------------------------------------------------------------------------
+// Phase schedule of the backward kernels
+//
+// Each wave works through its 32-row (dq) or 32-column (dk) sub-blocks in
+// alternating phases: an MFMA phase M(k) (GEMM1 of sub-block k, GEMM2 of
+// sub-block k-1) and a VALU phase V(k) (D of sub-block k).  M(k) reads its
+// LDS operands several MFMAs ahead; the two waves sharing a SIMD overlap one
+// wave's MFMA phase with the other's VALU phase as they drift.
+//
+// Tile ring: four single-tile buffers.  Tile t is read by M(2t) .. M(2t+2)
+// (GEMM2 of sub-block 2t+1 runs in M(2t+2)); V phases read at most the tile
+// of their own sub-block.
+// ----------------------------------------------------------------------------
+template <int kPerWave, bool kUniform>
+__device__ __forceinline__ void wait_first_tiles(int ntiles) {  // tile 0 landed, tiles 1 and 2 may be in flight
+  if (kUniform && ntiles >= 3)
+    wait_vmcnt<2 * kPerWave>();
+  else if (kUniform && ntiles == 2)
+    wait_vmcnt<kPerWave>();
+  else
+    wait_vmcnt<0>();
+}
+
+// Every wave runs M(0) V(0) M(1) .. freely; the workgroup meets once per
+// tile, before M(2t+2): tile t+1 has landed (each wave waits for its own
+// copies first), and every wave is past M(2t), the last reader of tile t-1,
+// whose buffer then receives tile t+3.  issue_part(t, j) issues part j
+// (student rows, teacher rows, side data) of tile t.
+template <int kPerWave, bool kUniform, typename MPhase, typename VPhase, typename IssuePart>
+__device__ __forceinline__ void free_run(int ntiles, MPhase mphase, VPhase vphase, IssuePart issue_part) {
+  for (int t = 0; t < 3 && t < ntiles; ++t)
+    for (int j = 0; j < 3; ++j) issue_part(t, j);
+  wait_first_tiles<kPerWave, kUniform>(ntiles);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    mphase(2 * t);
+    vphase(2 * t);
+    mphase(2 * t + 1);
+    vphase(2 * t + 1);
+    if (t + 1 < ntiles) {
+      if (kUniform && t + 2 < ntiles)
+        wait_vmcnt<kPerWave>();  // tile t+1 landed, tile t+2 in flight
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      if (t + 3 < ntiles)
+        for (int j = 0; j < 3; ++j) issue_part(t + 3, j);
+    }
+  }
+  mphase(2 * ntiles);  // GEMM2 of the last sub-block
+}
+
+// One MFMA phase of the backward: GEMM1 of a sub-block (S = A B^T for both
+// relations; A: this lane's rows of the student tile t1 at the offsets g1off
+// (the teacher tile follows it); B: register operands fb_s, fb_t) and GEMM2
+// of the previous sub-block (acc[db] += (rows of tile t2, transposed) x D).  With one wave per SIMD in
+// its MFMA phase, nothing hides LDS latency but the wave itself: the operand
+// reads run PD MFMAs ahead of their use, and scheduling barriers keep that
+// order.
+template <int DP, bool BF, int PD = 6>
+__device__ __forceinline__ void mfma_phase(const u16* t1, const unsigned* g1off, const u16x8* fb_s, const u16x8* fb_t,
+                                           f32x16& ss, f32x16& st, const u16* t2, int sb2, const TrOffsets<DP>& tro,
+                                           const u16x8* dop, f32x16* acc) {
+  constexpr int KS = DP / 16;
+  constexpr int NDB = DP >= 32 ? DP / 32 : 1;
+  constexpr int N1 = 2 * KS;       // GEMM1 MFMAs: student / teacher alternating
+  constexpr int N = N1 + 2 * NDB;  // then GEMM2: (m, db)
+  u16x8 op[N];
+  auto load = [&](int i) {
+    if (i < N1) {
+      op[i] = *reinterpret_cast<const u16x8*>(t1 + g1off[i >> 1] + ((i & 1) ? kTile * DP : 0));
+    } else {
+      const int j = i - N1;
+      op[i] = tro.read(t2, sb2, j / NDB, j % NDB);
+    }
+  };
+  ss = (f32x16)(0.f);
+  st = (f32x16)(0.f);
+#pragma unroll
+  for (int i = 0; i < PD && i < N; ++i) load(i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + PD < N) load(i + PD);
+    if (i < N1) {
+      if (i & 1)
+        st = mfma32<BF>(op[i], fb_t[i >> 1], st);
+      else
+        ss = mfma32<BF>(op[i], fb_s[i >> 1], ss);
+    } else {
+      const int j = i - N1;
+      acc[j % NDB] = mfma32<BF>(op[i], dop[j / NDB], acc[j % NDB]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ----------------------------------------------------------------------------
 // backward, row side: dq = sm_scale_s D K_s, one owner per query row
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
@@ -545,9 +717,8 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   constexpr int KS = DP / 16;
   constexpr int NDB = DP >= 32 ? DP / 32 : 1;  // 32-wide dim blocks of dq
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
-  constexpr int kBufs = 4;  // two tile pairs, one barrier per pair
-  __shared__ __attribute__((aligned(16))) u16 lks[kBufs][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[kBufs][kTile * DP];
+  constexpr int kBufs = 4;
+  __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];
 
   const int tid = threadIdx.x;
@@ -568,6 +739,9 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   const int causal = a.causal;
   const int diag_sb = (row0 >> 5) + w;
 
+  // Negative scales: flip the sign of q (exact) so the effective scale is
+  // positive and masked logits (kMaskedLogit) give exactly 0.
+  const u16 flip_s = a.s.scale < 0.f ? 0x8000 : 0, flip_t = a.t.scale < 0.f ? 0x8000 : 0;
   u16x8 fq_s[KS], fq_t[KS];
   {
     const u16* ps = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh + (int64_t)my_i * a.s.q_st;
@@ -576,15 +750,15 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
     for (int kk = 0; kk < KS; ++kk) {
       const int d0 = 16 * kk + 8 * half;
       const bool ld = in_range && d0 < a.s.dim;
-      fq_s[kk] = ld ? *reinterpret_cast<const u16x8*>(ps + d0) : (u16x8)(0);
-      fq_t[kk] = ld ? *reinterpret_cast<const u16x8*>(pt + d0) : (u16x8)(0);
+      fq_s[kk] = ld ? (*reinterpret_cast<const u16x8*>(ps + d0) ^ flip_s) : (u16x8)(0);
+      fq_t[kk] = ld ? (*reinterpret_cast<const u16x8*>(pt + d0) ^ flip_t) : (u16x8)(0);
     }
   }
   // Row normalisers in log2 units, -inf outside the valid set (exp2 -> 0).
   const float nls2 = in_range ? f.nl_s[(int64_t)bh * f.Tp + my_i] : kNegInf;
   const float nlt2 = in_range ? f.nl_t[(int64_t)bh * f.Tp + my_i] : kNegInf;
   const bool ok = nls2 != kNegInf;
-  const float c2s = a.s.scale2, c2t = a.t.scale2;
+  const float c2s = fabsf(a.s.scale2), c2t = fabsf(a.t.scale2);
   f32x16 dq[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dq[db] = (f32x16)(0.f);
@@ -596,67 +770,57 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
 
   const int nkt_all = f.Tp / kTile;
   const int ntiles = causal ? min(nkt_all, (row0 + kRows - 1) / kTile + 1) : nkt_all;
-  auto issue_tile = [&](int t) {
+  const int nsub = 2 * ntiles;
+  RowCopier<DP> cp_s, cp_t;
+  cp_s.init((int)a.s.k_st, a.s.dim, w, lane);
+  cp_t.init((int)a.t.k_st, a.t.dim, w, lane);
+  auto issue_part = [&](int t, int j) {
     const int buf = t % kBufs;
     const int j0 = t * kTile;
-    issue_rows<DP>(lks[buf], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
-    issue_rows<DP>(lkt[buf], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
-    issue_small(ltok[buf][w], tok + j0, lane);
+    if (j == 0)
+      cp_s.issue(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+    else if (j == 1)
+      cp_t.issue(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    else
+      issue_small(ltok[buf][w], tok + j0, lane);
   };
-  auto compute_tile = [&](int t) {
-    const int buf = t % kBufs;
-    const uint64_t tokmask = __ballot(ltok[buf][w][lane] != 0);  // bit j: key 64t + j valid
+  unsigned g1off[KS];  // this lane's row chunks of a tile: row l32 (+ 32 sb), chunk 2kk + half
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int gsb = 2 * t + sb;
-      if (causal && gsb > diag_sb) continue;
-      f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const int c = 2 * kk + half;
-        ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lks[buf], 32 * sb + l32, c)), fq_s[kk], ss);
-        st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lkt[buf], 32 * sb + l32, c)), fq_t[kk], st);
-      }
-      float dd[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dd[r] = fast_exp2(fmaf(ss[r], c2s, nls2)) - fast_exp2(fmaf(st[r], c2t, nlt2));
-      if (tokmask != ~0ull || (causal && gsb == diag_sb)) {
-        const unsigned bits = (unsigned)(tokmask >> (32 * sb + 4 * half));
-        const int lim = my_i - (t * kTile + 32 * sb + 4 * half);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int off = 8 * (r >> 2) + (r & 3);
-          dd[r] = (((bits >> off) & 1u) && (!causal || off <= lim)) ? dd[r] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const u16x8 bop = pack_d<BF>(dd + 8 * m);  // D cast to the input dtype (kernel_C.py:233)
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) dq[db] = mfma32<BF>(tr_operand<DP>(lks[buf], sb, m, db, lane), bop, dq[db]);
-      }
+  for (int kk = 0; kk < KS; ++kk) g1off[kk] = (unsigned)row_chunk_off<DP>(l32, 2 * kk + half);
+  TrOffsets<DP> tro;
+  tro.init(lane);
+
+  // Sub-block k = 2t + sb covers keys 32k .. 32k+31 (tile t, half sb).
+  // Sub-blocks above the causal diagonal are fully masked, not skipped (the
+  // wave holding the last rows, which has none, sets the pace).
+  f32x16 ss, st;     // scores of the sub-block between its M and V phase
+  uint64_t tm = 0;   // token validity of that sub-block's tile
+  u16x8 dop[2] = {(u16x8)(0), (u16x8)(0)};  // D of the previous sub-block, the B operand of GEMM2
+  // M(k): GEMM1 of sub-block k, GEMM2 of sub-block k-1 (dq += D K).  One
+  // code path for every k: M(0) multiplies a zero D, M(nsub) recomputes the
+  // scores of the last sub-block (still in LDS) and drops them.
+  auto mphase = [&](int k) {
+    const int k1 = min(k, nsub - 1), k2 = max(k - 1, 0);
+    const int buf = (k1 >> 1) % kBufs;
+    tm = __ballot(ltok[buf][w][lane] != 0);
+    mfma_phase<DP, BF>(lk[buf][0] + 32 * (k1 & 1) * DP, g1off, fq_s, fq_t, ss, st, lk[(k2 >> 1) % kBufs][0], k2 & 1,
+                       tro, dop, dq);
+  };
+  auto vphase = [&](int k) {
+    const int sb = k & 1;
+    if (tm != ~0ull || (causal && k >= diag_sb)) {
+      const int first = 32 * k + 4 * half;
+      mask_block(ss, st, (unsigned)(tm >> (32 * sb + 4 * half)), my_i - first, causal);
     }
+    float dd[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dd[r] = fast_exp2(fmaf(ss[r], c2s, nls2)) - fast_exp2(fmaf(st[r], c2t, nlt2));
+    dop[0] = pack_d<BF>(dd);  // D cast to the input dtype (kernel_C.py:233)
+    dop[1] = pack_d<BF>(dd + 8);
   };
 
   wait_vmcnt<0>();  // register operands landed before the ring starts
-  for (int t = 0; t < 4 && t < ntiles; ++t) issue_tile(t);
-  if (TC::kUniform && ntiles >= 4)
-    wait_vmcnt<2 * kPerWave>();
-  else if (TC::kUniform && ntiles == 3)
-    wait_vmcnt<kPerWave>();
-  else
-    wait_vmcnt<0>();
-  __syncthreads();
-  for (int p = 0; p < ntiles; p += 2) {
-    compute_tile(p);
-    if (p + 1 < ntiles) compute_tile(p + 1);
-    if (p + 2 < ntiles) {
-      wait_vmcnt<0>();
-      __syncthreads();
-      if (p + 4 < ntiles) issue_tile(p + 4);
-      if (p + 5 < ntiles) issue_tile(p + 5);
-    }
-  }
+  free_run<kPerWave, TC::kUniform>(ntiles, mphase, vphase, issue_part);
 
   if (in_range) {
     const float fs = ok ? a.s.scale * (a.dscale != nullptr ? *a.dscale : 1.f) : 0.f;
