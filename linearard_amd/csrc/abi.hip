@@ -172,6 +172,16 @@ bool hot_offsets_ok(std::initializer_list<const lard_tensor4*> ts, int64_t T) {
   return true;
 }
 
+// The throughput kernels give masked logits the raw value -1e30 and start
+// the forward's running maxima at -5e29; with the scales' magnitudes in
+// [1e-6, 1e6] and within a factor 1e6 of each other every masked
+// exponential is exactly 0 and every product stays finite.  Other scales
+// take the stage kernels.
+bool hot_scales_ok(float s, float t) {
+  const float as = std::fabs(s), at = std::fabs(t);
+  return as >= 1e-6f && at >= 1e-6f && as <= 1e6f && at <= 1e6f && as <= 1e6f * at && at <= 1e6f * as;
+}
+
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Carves 256-byte aligned regions out of a caller workspace in a fixed
@@ -448,11 +458,8 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
     const bool same = qs->dtype == qt->dtype;
     const bool bf = qs->dtype == LARD_DTYPE_BF16;
     const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
-    // the throughput forward keeps masked logits at -1e30 raw units: scales
-    // must be nonzero and moderate (|scale| <= 1e6) for that to stay exact
-    const bool scales_ok = sm_scale_s != 0.f && sm_scale_t != 0.f && std::fabs(sm_scale_s) <= 1e6f &&
-                           std::fabs(sm_scale_t) <= 1e6f;
-    const bool hot = lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T) && scales_ok;
+    const bool hot = lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T) &&
+                     hot_scales_ok(sm_scale_s, sm_scale_t);
     if (hot || lard::fused_fwd_supported(ds, dt, same)) {
       lard::HotArgs f{};
       fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
@@ -539,7 +546,8 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
   a.lse_t_in = lse_t;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int ds = (int)qs->size[3], dt = (int)qt->size[3];
-  if (lard::hot_supported(ds, dt, qs->dtype == qt->dtype) && hot_offsets_ok({qs, ks, qt, kt}, T)) {
+  if (lard::hot_supported(ds, dt, qs->dtype == qt->dtype) && hot_offsets_ok({qs, ks, qt, kt}, T) &&
+      hot_scales_ok(sm_scale_s, sm_scale_t)) {
     const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);

@@ -542,28 +542,9 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // G = l/16, u = l%16) points at row 16m + 8r + 4(G/2) + u/4, dims
 // 32db + 16(G%2) + 4(u%4) .. +3, so lane l receives, for dim 32db + l%32,
 // rows 16m + 8r + 4(l/32) + j: the k-slot order (0-3, 8-11, 4-7, 12-15) of
-// the accumulator registers that D comes from.
-template <int DP>
-__device__ __forceinline__ u16x8 tr_operand(const u16* tile, int sb, int m, int db, int lane) {
-  const int g = lane >> 4, u = lane & 15;
-  int dim = 32 * db + 16 * (g & 1) + 4 * (u & 3);
-  if (DP < 32) dim &= DP - 1;  // lanes whose output dims do not exist read in bounds
-  s16x4 v[2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = 32 * sb + 16 * m + 8 * r + 4 * (g >> 1) + (u >> 2);
-    const u16* p = row_chunk<DP>(tile, row, dim >> 3) + (dim & 7);
-    v[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(
-        (__attribute__((address_space(3))) u16*)p));
-  }
-  typedef short s16x8 __attribute__((ext_vector_type(8)));
-  const s16x8 both = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
-  return __builtin_bit_cast(u16x8, both);
-}
-
-// tr_operand with the per-lane offsets computed once: the operand of rows
-// 32sb + 16m .. and dims 32db .. is the tile base + a compile-time row offset
-// + off[r][db].
+// the accumulator registers that D comes from.  The per-lane part of each
+// address is computed once (off[r][db]); the rows 32sb + 16m add a
+// compile-time offset.
 template <int DP>
 struct TrOffsets {
   static constexpr int NDB = DP >= 32 ? DP / 32 : 1;
@@ -850,8 +831,7 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
   constexpr int NDB = DP >= 32 ? DP / 32 : 1;
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
   constexpr int kBufs = 4;
-  __shared__ __attribute__((aligned(16))) u16 lqs[kBufs][kTile * DP];
-  __shared__ __attribute__((aligned(16))) u16 lqt[kBufs][kTile * DP];
+  __shared__ __attribute__((aligned(16))) u16 lq[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   // per query row of the tile: -lse*log2(e) of student [0, 64) and teacher [64, 128)
   __shared__ __attribute__((aligned(16))) float lnl[kBufs][2 * kTile];
   static_assert(2 * kTile * sizeof(float) == kWaves * 64, "one 64-byte row-data copy per wave");
@@ -895,6 +875,11 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
   // fill serves the XCD), instead of each starting at its own diagonal.
   const int ntiles = causal ? ntile_all - (cb * kRows) / kTile : ntile_all;
   auto tile_of = [&](int it) { return ntile_all - 1 - it; };
+  RowCopier<DP> cp_s, cp_t;
+  cp_s.init((int)a.s.q_st, a.s.dim, w, lane);
+  cp_t.init((int)a.t.q_st, a.t.dim, w, lane);
+  TrOffsets<DP> tro;
+  tro.init(lane);
   int loaded_ht = -1;
 
   for (int hh = 0; hh < a.s.group; ++hh) {
@@ -918,8 +903,8 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
     auto issue_tile = [&](int it) {
       const int buf = it % kBufs;
       const int i0 = tile_of(it) * kTile;
-      issue_rows<DP>(lqs[buf], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
-      issue_rows<DP>(lqt[buf], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
+      cp_s.issue(lq[buf][0], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
+      cp_t.issue(lq[buf][1], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
       issue_small(&lnl[buf][16 * w], nl_src + i0, lane);
     };
     auto compute_tile = [&](int it) {
@@ -929,13 +914,8 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
       for (int sb = 0; sb < 2; ++sb) {
         const int gsb = 2 * t + sb;
         if (causal && gsb < diag_sb) continue;
-        f32x16 ss = (f32x16)(0.f), st = (f32x16)(0.f);
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-          const int c = 2 * kk + half;
-          ss = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lqs[buf], 32 * sb + l32, c)), fk_s[kk], ss);
-          st = mfma32<BF>(*reinterpret_cast<const u16x8*>(row_chunk<DP>(lqt[buf], 32 * sb + l32, c)), fk_t[kk], st);
-        }
+        f32x16 ss, st;
+        sub_scores<DP, BF>(lq[buf][0], 32 * sb, l32, half, fk_s, fk_t, ss, st);
         float dd[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
@@ -959,7 +939,7 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
           const u16x8 bop = pack_d<BF>(dd + 8 * m);  // D cast to the input dtype (kernel_C.py:233)
 #pragma unroll
           for (int db = 0; db < NDB; ++db)
-            dk[db] = mfma32<BF>(tr_operand<DP>(lqs[buf], sb, m, db, lane), bop, dk[db]);
+            dk[db] = mfma32<BF>(tro.read(lq[buf][0], sb, m, db), bop, dk[db]);
         }
       }
     };

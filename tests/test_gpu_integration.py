@@ -190,9 +190,11 @@ def test_hot_path_gqa_masked(gpu_available, causal):
         assert np.abs(g - ref).max() / np.abs(ref).max() <= 2e-2
 
 
-@pytest.mark.parametrize("a_s,a_t", [(-0.09, -0.09), (0.05, -0.12), (0.3, 0.02)])
+@pytest.mark.parametrize("a_s,a_t", [(-0.09, -0.09), (0.05, -0.12), (0.3, 0.02), (3e-7, 0.1), (1e-4, 150.0)])
 def test_hot_path_signed_and_unequal_scales(gpu_available, a_s, a_t):
-    """Scales of either sign and ratio (the reference accepts any finite scale)."""
+    """Scales of either sign and ratio (the reference accepts any finite scale).
+    The last two cases (a scale below 1e-6, a ratio above 1e6) take the stage
+    kernels instead of the throughput kernels."""
     from linearard_amd.attention_KL import attn_kl_align
 
     rng = np.random.default_rng(7)
