@@ -25,6 +25,7 @@ WRITE_SIZE runs of this script with --copy-calibration, scaled by a plain
 copy of known size), else null.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg4]
+    python bench.py --workload layers [--layers 4]   # batched relation loss vs the per-call loop
 """
 
 from __future__ import annotations
@@ -77,6 +78,31 @@ def rope_pair(B, H, n, d, pos_scale, base, seed=0, outliers=4):
     return rotate(pos / pos_scale), rotate(pos)  # student, teacher
 
 
+def rope_pair_ntk(B, H, n, d, base, base_scale, seed=0, outliers=4):
+    """Teacher/student pair for SURVEY cfg3: the same pre-RoPE vectors with
+    per-head std ~ U(0.5, 2), rotated at positions p with RoPE base `base`
+    (teacher) and `base * base_scale` (student), HF rotate_half layout."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randn((B, H, n, d), generator=g, dtype=torch.float32)
+    v *= (0.5 + 1.5 * torch.rand((1, H, 1, 1), generator=g))
+    if outliers:
+        idx = torch.randperm(d, generator=g)[:outliers]
+        v[..., idx] *= 20.0 / math.sqrt(d)
+    pos = torch.arange(n, dtype=torch.float64)
+
+    def rotate(b):
+        inv_freq = b ** (-torch.arange(0, d, 2, dtype=torch.float64) / d)
+        ang = torch.outer(pos, inv_freq)
+        cos = torch.cat([ang.cos(), ang.cos()], -1).float()
+        sin = torch.cat([ang.sin(), ang.sin()], -1).float()
+        x1, x2 = v[..., : d // 2], v[..., d // 2:]
+        return (v * cos + torch.cat([-x2, x1], -1) * sin).to(torch.bfloat16)
+
+    return rotate(base * base_scale), rotate(base)  # student, teacher
+
+
 def algorithmic_flops(B, H, n, d):
     pairs = n * (n + 1) // 2
     return 12 * d * pairs * B * H
@@ -119,6 +145,78 @@ def traffic_summary(config):
         return json.load(f)
 
 
+def run_layers(args):
+    """The train.py relation loss (Q/Q + K/K + V/V per layer, train.py:369-410)
+    over `--layers` layers at SURVEY cfg3's shapes (B=1, n=8192, d=128, Q/Q
+    32 heads, K/K and V/V 8 heads; teacher RoPE base 5e5, student base x8),
+    fwd+bwd, two ways: the batched launches (relation_kl_loss) and the
+    reference caller's loop of attn_kl_align calls."""
+    import torch
+
+    from linearard_amd.attention_KL import attn_kl_align, relation_kl_loss
+
+    B, n, d, Hq, Hkv, layers = 1, 8192, 128, 32, 8, args.layers
+    dev = torch.device("cuda", 0)
+    S, Tt = [], []
+    for layer in range(layers):
+        s_, t_ = [], []
+        for j, H in enumerate((Hq, Hkv, Hkv)):
+            xs, xt = rope_pair_ntk(B, H, n, d, 5e5, 8.0, seed=100 * layer + j)
+            s_.append(xs.to(dev).requires_grad_(True))
+            t_.append(xt.to(dev))
+        S.append(s_)
+        Tt.append(t_)
+    scale = d ** -0.5
+
+    def batched():
+        return relation_kl_loss([l[0] for l in S], [l[1] for l in S], [l[2] for l in S],
+                                [l[0] for l in Tt], [l[1] for l in Tt], [l[2] for l in Tt],
+                                sm_scale_s=scale, sm_scale_t=scale)
+
+    def loop():  # train.py:369-410 as written
+        q = k = v = 0.0
+        for li in range(layers):
+            denom = B * Hq * n
+            out = [attn_kl_align(S[li][j], S[li][j], Tt[li][j], Tt[li][j], attn_mask=None, causal=True,
+                                 sm_scale_s=scale, sm_scale_t=scale) for j in range(3)]
+            q, k, v = q + out[0] / denom, k + out[1] / denom, v + out[2] / denom
+        return (q + k + v) / max(1, layers)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn().backward()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            loss = fn()
+            loss.backward()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps * 1e3, float(loss.item())
+
+    ms_b, loss_b = timed(batched)
+    ms_l, loss_l = timed(loop)
+    rows = layers * B * (Hq + 2 * Hkv) * n
+    flops = layers * (algorithmic_flops(B, Hq, n, d) + 2 * algorithmic_flops(B, Hkv, n, d))
+    print(json.dumps({
+        "metric": "attention-relation loss (Q/Q+K/K+V/V per layer) fwd+bwd relation-tokens/sec, batched launches",
+        "value": rows / (ms_b * 1e-3),
+        "unit": "relation-tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_b,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian pre-RoPE vectors, per-head std U(0.5,2), RoPE teacher base 5e5, "
+                "student base x8)",
+        "config": {"workload": f"cfg3 relation loss: {layers} layers x (Q/Q {Hq} heads, K/K {Hkv}, V/V {Hkv}), "
+                               f"B={B}, n={n}, d={d}, causal", "layers": layers, "B": B, "n": n, "d": d},
+        "tflops": flops / (ms_b * 1e-3) / 1e12,
+        "frac_bf16_peak": flops / (ms_b * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS,
+        "loop_ms_per_step": ms_l,
+        "loop_value": rows / (ms_l * 1e-3),
+        "speedup_vs_loop": ms_l / ms_b,
+        "loss": loss_b,
+        "loop_loss": loss_l,
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,12 +226,19 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (counter-scale calibration)")
+    ap.add_argument("--workload", default="relation", choices=("relation", "layers"),
+                    help="relation: one self relation at --config (the headline); layers: the train.py "
+                         "relation loss over --layers layers at cfg3 shapes, batched vs the per-call loop")
+    ap.add_argument("--layers", type=int, default=4)
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; the multi-GPU sharding is a design note "
                                    "(DESIGN.md), not a launched path", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.workload == "layers":
+        run_layers(args)
+        return
 
     import torch
 

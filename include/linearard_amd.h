@@ -144,6 +144,53 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                           const float* dloss, int self_relation, float* dq_out, float* dk_out,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * One self relation of a batched relation loss: the student tensor xs is
+ * both q and k, the teacher tensor xt likewise -- the call
+ * attn_kl_align(x_s, x_s, x_t, x_t) of train.py:380-402.  lse_s / lse_t
+ * [B, H, T] float32 are written by the batched forward and read by the
+ * batched backward; dxs [B, H, T, D] float32 receives the gradient of xs.
+ */
+typedef struct lard_relation {
+  lard_tensor4 xs;
+  lard_tensor4 xt;
+  float* lse_s;
+  float* lse_t;
+  float* dxs;
+} lard_relation;
+
+/* Workspace of lard_attn_kl_batched_forward and _backward (bytes, the same
+ * for both): per-row KL terms of every relation, the loss-sum partials, one
+ * validity byte per token and two row normalisers per query row. */
+size_t lard_attn_kl_batched_workspace_bytes(const lard_relation* rels, int nrel);
+
+/*
+ * Batched forward -- replaces the caller's loop of attn_kl_align calls over
+ * layers and Q/K/V relations (train.py:369-410) with one launch per
+ * 8 relations (head counts may differ, as Q/Q 32 vs K/K 8 heads):
+ *   loss_out[0] = sum_r weights[r] * KL_r,
+ * KL_r the relation's loss as lard_attn_kl_forward computes it (a sum over
+ * rows), weights a device float32 [nrel] array or NULL (all 1), the whole
+ * sum one deterministic reduction.  All relations share B, T, the dtype and
+ * the head dim (Ds == Dt <= 128); scales must lie in [1e-6, 1e6] within a
+ * factor 1e6 of each other.  Other batches are LARD_ERR_UNSUPPORTED and go
+ * relation by relation through lard_attn_kl_forward.
+ */
+int lard_attn_kl_batched_forward(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                 float sm_scale_s, float sm_scale_t, const float* weights, float* loss_out,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Batched backward -- AttnKLAlignFn.backward (integration.py:48-67) of every
+ * relation of the batched forward, from the LSE vectors it wrote:
+ *   rels[r].dxs = dloss * weights[r] * dKL_r / dxs
+ * (dloss a device float32 scalar or NULL for 1), each the whole gradient of
+ * xs (row and column side summed), bitwise deterministic.
+ */
+int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                  float sm_scale_s, float sm_scale_t, const float* weights, const float* dloss,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
 /* Kernel ids of the timing hook. */
 #define LARD_KERNEL_FORWARD 0  /* one-pass forward: both LSEs and the per-row KL */
 #define LARD_KERNEL_ROW_GRAD 1 /* backward, row side: dq (kernel_C.py:224-239) */
@@ -154,10 +201,10 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
  * Timing hook for measurement harnesses -- no counterpart in the reference
  * (its kernels are timed from outside).  While enabled, every launch of the
  * three kernels above by lard_attn_kl_forward / lard_attn_kl_backward /
- * lard_kl_backward is bracketed by two HIP events recorded on its launch
- * stream.  lard_timing_read() waits for the recorded events and returns the
- * summed elapsed milliseconds and the launch count of one kernel since its
- * last read, then clears them.  Off by default.  While enabled, launches
+ * lard_kl_backward / lard_attn_kl_batched_* is bracketed by two HIP events
+ * recorded on its launch stream.  lard_timing_read() waits for the recorded
+ * events and returns the summed elapsed milliseconds and the launch count of
+ * one kernel since its last read, then clears them.  Off by default.  While enabled, launches
  * cannot be captured into a HIP graph and calls from several host threads
  * serialise briefly on one lock.
  */

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(PACKAGE_DIR, "liblinearard_amd.so")
 HEADER_PATH = os.path.join(os.path.dirname(PACKAGE_DIR), "include", "linearard_amd.h")
 
 LARD_OK = 0
+LARD_ERR_UNSUPPORTED = -2
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 MASK_CODES = {torch.bool: 1, torch.uint8: 1, torch.int32: 2, torch.int64: 3}
 
@@ -46,8 +47,21 @@ class Mask(ctypes.Structure):
     ]
 
 
+class Relation(ctypes.Structure):
+    """``lard_relation``: one self relation of a batched loss."""
+
+    _fields_ = [
+        ("xs", Tensor4),
+        ("xt", Tensor4),
+        ("lse_s", ctypes.c_void_p),
+        ("lse_t", ctypes.c_void_p),
+        ("dxs", ctypes.c_void_p),
+    ]
+
+
 _T4P = ctypes.POINTER(Tensor4)
 _MP = ctypes.POINTER(Mask)
+_RP = ctypes.POINTER(Relation)
 _FP = ctypes.c_void_p  # float* device pointers are passed as addresses
 
 # name -> (restype, argtypes); must cover every function include/linearard_amd.h declares.
@@ -68,6 +82,13 @@ SIGNATURES = {
     "lard_attn_kl_backward": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, _FP, ctypes.c_int, _FP, _FP, ctypes.c_void_p,
                                              ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_attn_kl_batched_workspace_bytes": (ctypes.c_size_t, [_RP, ctypes.c_int]),
+    "lard_attn_kl_batched_forward": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
+                                                    ctypes.c_float, _FP, _FP, ctypes.c_void_p, ctypes.c_size_t,
+                                                    ctypes.c_void_p]),
+    "lard_attn_kl_batched_backward": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
+                                                     ctypes.c_float, _FP, _FP, ctypes.c_void_p, ctypes.c_size_t,
+                                                     ctypes.c_void_p]),
     "lard_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "lard_timing_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                         ctypes.POINTER(ctypes.c_int64)]),

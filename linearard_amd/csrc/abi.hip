@@ -304,6 +304,79 @@ hipError_t timed(int kernel, hipStream_t st, F&& launch) {
   return e;
 }
 
+
+// ---- batched relation loss (lard_attn_kl_batched_*) ----
+
+// per-row KL terms of every relation, loss partials, token validity (shared:
+// one B and T), row normalisers of every relation
+struct BatchWs {
+  LossWs loss;
+  unsigned char* tok_ok;
+  float* nl_s;
+  float* nl_t;
+};
+
+int64_t rel_rows(const lard_relation& r) { return r.xs.size[0] * r.xs.size[1] * r.xs.size[2]; }
+
+BatchWs batch_layout(void* base, const lard_relation* rels, int nrel, size_t* bytes) {
+  int64_t rows = 0, prows = 0;
+  for (int r = 0; r < nrel; ++r) {
+    rows += rel_rows(rels[r]);
+    prows += rels[r].xs.size[0] * rels[r].xs.size[1] * padded_len(rels[r].xs.size[2]);
+  }
+  size_t loss_bytes = 0;
+  BatchWs w;
+  w.loss = loss_layout(base, rows, &loss_bytes);
+  Carver c(base != nullptr ? static_cast<char*>(base) + loss_bytes : nullptr);
+  w.tok_ok = c.take<unsigned char>(rels[0].xs.size[0] * padded_len(rels[0].xs.size[2]));
+  w.nl_s = c.take<float>(prows);
+  w.nl_t = c.take<float>(prows);
+  if (bytes != nullptr) *bytes = loss_bytes + c.bytes();
+  return w;
+}
+
+// A batch the throughput kernels take: self relations sharing B, T, dtype
+// and head dim D <= 128, moderate scales.  Everything else is rejected.
+int check_batch(const lard_relation* rels, int nrel, const lard_mask* mask, float sm_scale_s, float sm_scale_t) {
+  int rc;
+  if (rels == nullptr || nrel < 1) return fail(LARD_ERR_INVALID_ARGUMENT, "rels must hold at least one relation");
+  const lard_tensor4& x0 = rels[0].xs;
+  for (int r = 0; r < nrel; ++r) {
+    const lard_tensor4& xs = rels[r].xs;
+    const lard_tensor4& xt = rels[r].xt;
+    if ((rc = check_pair(&xs, &xs, "xs", "xs")) != LARD_OK) return rc;
+    if ((rc = check_pair(&xt, &xt, "xt", "xt")) != LARD_OK) return rc;
+    if (xs.size[0] != xt.size[0] || xs.size[1] != xt.size[1] || xs.size[2] != xt.size[2])
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: student/teacher B/H/T must align", r);
+    if (xs.size[0] != x0.size[0] || xs.size[2] != x0.size[2])
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: every relation must share B and T", r);
+    if (xs.dtype != x0.dtype || xt.dtype != x0.dtype || xs.size[3] != x0.size[3] || xt.size[3] != x0.size[3])
+      return fail(LARD_ERR_UNSUPPORTED, "relation %d: batched relations must share the dtype and head dim", r);
+    if (!lard::hot_supported((int)xs.size[3], (int)xt.size[3], true) || !hot_offsets_ok({&xs, &xt}, xs.size[2]))
+      return fail(LARD_ERR_UNSUPPORTED, "relation %d: shape outside the batched kernels (D <= 128)", r);
+    if (xs.size[1] <= 0) return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d has no heads", r);
+    if ((rc = check_blocks(xs.size[0], xs.size[1], xs.size[2])) != LARD_OK) return rc;
+  }
+  if ((rc = check_mask(mask, x0.size[0], x0.size[2])) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_s, "sm_scale_s")) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_t, "sm_scale_t")) != LARD_OK) return rc;
+  if (!hot_scales_ok(sm_scale_s, sm_scale_t))
+    return fail(LARD_ERR_UNSUPPORTED, "scales outside the batched kernels' range");
+  return LARD_OK;
+}
+
+lard::HotArgs relation_args(const lard_relation& R, const lard_mask* mask, int causal, float sm_scale_s,
+                            float sm_scale_t, int Tp, const unsigned char* tok_ok) {
+  lard::HotArgs f{};
+  const int64_t H = R.xs.size[1];
+  fill_side(f.r.s, &R.xs, &R.xs, H, sm_scale_s);
+  fill_side(f.r.t, &R.xt, &R.xt, H, sm_scale_t);
+  fill_common(f.r, R.xs.size[0], H, R.xs.size[2], mask, causal);
+  f.Tp = Tp;
+  f.tok_ok = tok_ok;
+  return f;
+}
+
 }  // namespace
 
 extern "C" {
@@ -592,3 +665,125 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
 }
 
 }  // extern "C"
+
+size_t lard_attn_kl_batched_workspace_bytes(const lard_relation* rels, int nrel) {
+  if (rels == nullptr || nrel < 1) return 0;
+  size_t bytes = 0;
+  batch_layout(nullptr, rels, nrel, &bytes);
+  return bytes;
+}
+
+int lard_attn_kl_batched_forward(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                 float sm_scale_s, float sm_scale_t, const float* weights, float* loss_out,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_batch(rels, nrel, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  if (loss_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "loss_out must not be NULL");
+  int64_t rows = 0;
+  for (int r = 0; r < nrel; ++r) {
+    if (rel_rows(rels[r]) > 0 && (rels[r].lse_s == nullptr || rels[r].lse_t == nullptr))
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: lse outputs must not be NULL", r);
+    rows += rel_rows(rels[r]);
+  }
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0)
+    return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "batched forward reduce launch");
+  const size_t need = lard_attn_kl_batched_workspace_bytes(rels, nrel);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  const BatchWs w = batch_layout(workspace, rels, nrel, nullptr);
+  const int Tp = (int)padded_len(rels[0].xs.size[2]);
+  const int dp = padded_dim(rels[0].xs.size[3]);
+  const bool bf = rels[0].xs.dtype == LARD_DTYPE_BF16;
+  {
+    const lard::HotArgs f0 = relation_args(rels[0], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok);
+    if ((rc = hip_status(lard::launch_token_prep(f0.r, Tp, w.tok_ok, st), "batched forward token prep launch")) !=
+        LARD_OK)
+      return rc;
+  }
+  int64_t row_off = 0;
+  for (int g = 0; g < nrel; g += lard::kMaxRelations) {
+    lard::HotBatch m{};
+    for (int r = g; r < nrel && r < g + lard::kMaxRelations; ++r) {
+      if (rel_rows(rels[r]) == 0) continue;
+      lard::HotArgs f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok);
+      f.lse_s_out = rels[r].lse_s;
+      f.lse_t_out = rels[r].lse_t;
+      f.row_out = w.loss.rows + row_off;
+      f.r.weight = weights != nullptr ? weights + r : nullptr;
+      row_off += rel_rows(rels[r]);
+      m.rel[m.n++] = f;
+    }
+    if (m.n == 0) continue;
+    if ((rc = hip_status(timed(LARD_KERNEL_FORWARD, st, [&] { return lard::launch_hot_fwd_batch(m, dp, bf, st); }),
+                         "batched forward launch")) != LARD_OK)
+      return rc;
+  }
+  return hip_status(lard::launch_reduce_sum(w.loss.rows, rows, w.loss.partial, loss_out, st),
+                    "batched forward reduce launch");
+}
+
+int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                  float sm_scale_s, float sm_scale_t, const float* weights, const float* dloss,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_batch(rels, nrel, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  int64_t rows = 0;
+  for (int r = 0; r < nrel; ++r) {
+    if (rel_rows(rels[r]) > 0 && (rels[r].lse_s == nullptr || rels[r].lse_t == nullptr || rels[r].dxs == nullptr))
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: lse inputs and dxs must not be NULL", r);
+    rows += rel_rows(rels[r]);
+  }
+  if (rows == 0) return ok();
+  const size_t need = lard_attn_kl_batched_workspace_bytes(rels, nrel);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const BatchWs w = batch_layout(workspace, rels, nrel, nullptr);
+  const int Tp = (int)padded_len(rels[0].xs.size[2]);
+  const int dp = padded_dim(rels[0].xs.size[3]);
+  const bool bf = rels[0].xs.dtype == LARD_DTYPE_BF16;
+  std::vector<lard::HotArgs> fs((size_t)nrel);
+  int64_t nl_off = 0;
+  for (int r = 0; r < nrel; ++r) {
+    lard::HotArgs& f = fs[(size_t)r];
+    f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok);
+    f.r.lse_s_in = rels[r].lse_s;
+    f.r.lse_t_in = rels[r].lse_t;
+    float* nl_s = w.nl_s + nl_off;
+    float* nl_t = w.nl_t + nl_off;
+    f.nl_s = nl_s;
+    f.nl_t = nl_t;
+    nl_off += rels[r].xs.size[0] * rels[r].xs.size[1] * (int64_t)Tp;
+    if (r == 0 && (rc = hip_status(lard::launch_token_prep(f.r, Tp, w.tok_ok, st),
+                                   "batched backward token prep launch")) != LARD_OK)
+      return rc;
+    if (rel_rows(rels[r]) > 0 && (rc = hip_status(lard::launch_row_prep(f.r, Tp, w.tok_ok, nl_s, nl_t, st),
+                                                  "batched backward row prep launch")) != LARD_OK)
+      return rc;
+  }
+  for (int g = 0; g < nrel; g += lard::kMaxRelations) {
+    // row side first (into dxs), then the column side, which adds it in place
+    // and applies dloss * weight once
+    lard::HotBatch mq{}, mk{};
+    for (int r = g; r < nrel && r < g + lard::kMaxRelations; ++r) {
+      if (rel_rows(rels[r]) == 0) continue;
+      lard::HotArgs f = fs[(size_t)r];
+      f.dq_out = rels[r].dxs;
+      mq.rel[mq.n++] = f;
+      f.r.dk_out = rels[r].dxs;
+      f.r.dk_add = rels[r].dxs;
+      f.r.dscale = dloss;
+      f.r.weight = weights != nullptr ? weights + r : nullptr;
+      mk.rel[mk.n++] = f;
+    }
+    if (mq.n == 0) continue;
+    if ((rc = hip_status(timed(LARD_KERNEL_ROW_GRAD, st, [&] { return lard::launch_hot_dq_batch(mq, dp, bf, st); }),
+                         "batched backward dq launch")) != LARD_OK)
+      return rc;
+    if ((rc = hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_hot_bwd_batch(mk, dp, bf, st); }),
+                         "batched backward dk launch")) != LARD_OK)
+      return rc;
+  }
+  return ok();
+}

@@ -65,6 +65,54 @@ LARD_HOT_DISPATCH(hot_dq_kernel)
 LARD_HOT_DISPATCH(hot_bwd_kernel)
 #undef LARD_HOT_DISPATCH
 
+#define LARD_HOT_BATCH_DISPATCH(KERNEL)                                                              \
+  template <bool BF>                                                                                 \
+  static hipError_t KERNEL##_dispatch(const HotBatch& m, int dp, hipStream_t stream) {              \
+    const dim3 grid(m.first[m.n]), block(kWaves * 64);                                               \
+    switch (dp) {                                                                                    \
+      case 16: hipLaunchKernelGGL((KERNEL<16, BF>), grid, block, 0, stream, m); break;               \
+      case 32: hipLaunchKernelGGL((KERNEL<32, BF>), grid, block, 0, stream, m); break;               \
+      case 64: hipLaunchKernelGGL((KERNEL<64, BF>), grid, block, 0, stream, m); break;               \
+      case 128: hipLaunchKernelGGL((KERNEL<128, BF>), grid, block, 0, stream, m); break;             \
+      default: return hipErrorInvalidValue;                                                          \
+    }                                                                                                \
+    return hipGetLastError();                                                                        \
+  }
+
+LARD_HOT_BATCH_DISPATCH(hot_fwd_batch_kernel)
+LARD_HOT_BATCH_DISPATCH(hot_dq_batch_kernel)
+LARD_HOT_BATCH_DISPATCH(hot_bwd_batch_kernel)
+#undef LARD_HOT_BATCH_DISPATCH
+
+// first[] from the relations' work items; false if the batch is empty,
+// too large or its grid would not fit an int.
+static bool batch_prefix(HotBatch& m, bool column_side) {
+  if (m.n < 1 || m.n > kMaxRelations) return false;
+  int64_t total = 0;
+  for (int r = 0; r < m.n; ++r) {
+    m.first[r] = (int)total;
+    total += column_side ? bwd_items(m.rel[r]) : fwd_items(m.rel[r]);
+    if (total > INT32_MAX) return false;
+  }
+  m.first[m.n] = (int)total;
+  return total > 0;
+}
+
+hipError_t launch_hot_fwd_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream) {
+  if (!batch_prefix(m, false)) return hipErrorInvalidValue;
+  return bf16 ? hot_fwd_batch_kernel_dispatch<true>(m, dp, stream) : hot_fwd_batch_kernel_dispatch<false>(m, dp, stream);
+}
+
+hipError_t launch_hot_dq_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream) {
+  if (!batch_prefix(m, false)) return hipErrorInvalidValue;
+  return bf16 ? hot_dq_batch_kernel_dispatch<true>(m, dp, stream) : hot_dq_batch_kernel_dispatch<false>(m, dp, stream);
+}
+
+hipError_t launch_hot_bwd_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream) {
+  if (!batch_prefix(m, true)) return hipErrorInvalidValue;
+  return bf16 ? hot_bwd_batch_kernel_dispatch<true>(m, dp, stream) : hot_bwd_batch_kernel_dispatch<false>(m, dp, stream);
+}
+
 static int row_blocks(const RelArgs& a, int heads) { return (a.T + kRows - 1) / kRows * a.B * heads; }
 
 hipError_t launch_hot_fwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream) {

@@ -368,7 +368,7 @@ __device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int
 }
 
 template <int DP, bool BF>
-__global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
+__device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   const RelArgs& a = f.r;
   using TC = TileCopies<DP>;
   constexpr int KS = DP / 16;
@@ -386,7 +386,6 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
   const int l32 = lane & 31;
   const int T = a.T;
   const int nrb = (T + kRows - 1) / kRows;
-  const int item = xcd_item(blockIdx.x, nrb * a.B * a.Hq);
   const int bh = item / nrb;
   const int rb = nrb - 1 - (item - bh * nrb);  // longest causal rows first
   const int b = bh / a.Hq;
@@ -522,7 +521,8 @@ __global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
     f.lse_s_out[row_index] = row_valid ? (l_s > 0.f ? (xs + lg_s) * kLn2 : kNegInf) : 0.f;
     f.lse_t_out[row_index] = row_valid ? (l_t > 0.f ? (xt + lg_t) * kLn2 : kNegInf) : 0.f;
     // KL = E_pt[x_t - x_s] + (max_s - max_t) + ln(l_s / l_t); no two rounded LSEs are subtracted
-    f.row_out[row_index] = ok ? (acc * c2s / l_t + (xs - xt) + (lg_s - lg_t)) * kLn2 : 0.f;
+    const float wr = a.weight != nullptr ? *a.weight : 1.f;
+    f.row_out[row_index] = ok ? (acc * c2s / l_t + (xs - xt) + (lg_s - lg_t)) * kLn2 * wr : 0.f;
   }
 }
 
@@ -692,7 +692,7 @@ __device__ __forceinline__ void mfma_phase(const u16* t1, const unsigned* g1off,
 // backward, row side: dq = sm_scale_s D K_s, one owner per query row
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
-__global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
+__device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
   const RelArgs& a = f.r;
   using TC = TileCopies<DP>;
   constexpr int KS = DP / 16;
@@ -709,7 +709,6 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   const int l32 = lane & 31;
   const int T = a.T;
   const int nrb = (T + kRows - 1) / kRows;
-  const int item = xcd_item(blockIdx.x, nrb * a.B * a.Hq);
   const int bh = item / nrb;
   const int rb = nrb - 1 - (item - bh * nrb);
   const int b = bh / a.Hq;
@@ -804,7 +803,8 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
   free_run<kPerWave, TC::kUniform>(ntiles, mphase, vphase, issue_part);
 
   if (in_range) {
-    const float fs = ok ? a.s.scale * (a.dscale != nullptr ? *a.dscale : 1.f) : 0.f;
+    const float fs =
+        ok ? a.s.scale * (a.dscale != nullptr ? *a.dscale * (a.weight != nullptr ? *a.weight : 1.f) : 1.f) : 0.f;
     float* out = f.dq_out + ((int64_t)bh * T + my_i) * a.s.dim;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -824,7 +824,7 @@ __global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
 // backward, column side: dk = sm_scale_s sum_{h in group} D^T Q_s
 // ----------------------------------------------------------------------------
 template <int DP, bool BF>
-__global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
+__device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
   const RelArgs& a = f.r;
   using TC = TileCopies<DP>;
   constexpr int KS = DP / 16;
@@ -843,7 +843,6 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
   const int l32 = lane & 31;
   const int T = a.T;
   const int ncb = (T + kRows - 1) / kRows;
-  const int item = xcd_item(blockIdx.x, ncb * a.B * a.s.hkv);
   const int bg = item / ncb;
   const int cb = item - bg * ncb;  // small cb = longest causal columns first
   const int b = bg / a.s.hkv;
@@ -970,7 +969,7 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
     const int64_t off = ((int64_t)bg * T + my_j) * a.s.dim;
     float* out = a.dk_out + off;
     const float fs = a.s.scale;
-    const float mult = a.dscale != nullptr ? *a.dscale : 1.f;
+    const float mult = (a.dscale != nullptr ? *a.dscale : 1.f) * (a.weight != nullptr ? *a.weight : 1.f);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -980,12 +979,70 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
           f32x4 v = {dk[db][4 * gq] * fs, dk[db][4 * gq + 1] * fs, dk[db][4 * gq + 2] * fs, dk[db][4 * gq + 3] * fs};
           if (!col_valid) v = (f32x4)(0.f);  // masked key columns get no gradient (kernel_C.py:252-253)
           if (a.dk_add != nullptr) v += *reinterpret_cast<const f32x4*>(a.dk_add + off + d0);
-          if (a.dscale != nullptr) v *= mult;
+          if (a.dscale != nullptr || a.weight != nullptr) v *= mult;
           *reinterpret_cast<f32x4*>(out + d0) = v;
         }
       }
     }
   }
+}
+
+// ----------------------------------------------------------------------------
+// launch forms: one relation, or a batch of up to kMaxRelations relations in
+// one grid (train.py:369-410 runs Q/Q, K/K and V/V of every layer; their
+// head counts differ).  The batch travels in the kernel arguments, so a
+// launch needs no device copy of it and stays valid under graph capture.
+// ----------------------------------------------------------------------------
+constexpr int kMaxRelations = 8;
+
+struct HotBatch {
+  int n;                          // relations
+  int first[kMaxRelations + 1];   // work items before relation r; first[n] = total
+  HotArgs rel[kMaxRelations];
+};
+
+// work items (workgroups) of one relation: row blocks x B x heads
+__host__ __device__ inline int fwd_items(const HotArgs& f) { return (f.r.T + kRows - 1) / kRows * f.r.B * f.r.Hq; }
+__host__ __device__ inline int bwd_items(const HotArgs& f) {
+  return (f.r.T + kRows - 1) / kRows * f.r.B * f.r.s.hkv;
+}
+
+// relation r of batch item g (uniform: a short scalar loop)
+__device__ __forceinline__ int batch_relation(const HotBatch& m, int g) {
+  int r = 0;
+  while (r + 1 < m.n && g >= m.first[r + 1]) ++r;
+  return r;
+}
+
+template <int DP, bool BF>
+__global__ __launch_bounds__(kWaves * 64) void hot_fwd_kernel(const HotArgs f) {
+  hot_fwd_body<DP, BF>(f, xcd_item(blockIdx.x, fwd_items(f)));
+}
+template <int DP, bool BF>
+__global__ __launch_bounds__(kWaves * 64) void hot_dq_kernel(const HotArgs f) {
+  hot_dq_body<DP, BF>(f, xcd_item(blockIdx.x, fwd_items(f)));
+}
+template <int DP, bool BF>
+__global__ __launch_bounds__(kWaves * 64) void hot_bwd_kernel(const HotArgs f) {
+  hot_bwd_body<DP, BF>(f, xcd_item(blockIdx.x, bwd_items(f)));
+}
+template <int DP, bool BF>
+__global__ __launch_bounds__(kWaves * 64) void hot_fwd_batch_kernel(const HotBatch m) {
+  const int g = xcd_item(blockIdx.x, m.first[m.n]);
+  const int r = batch_relation(m, g);
+  hot_fwd_body<DP, BF>(m.rel[r], g - m.first[r]);
+}
+template <int DP, bool BF>
+__global__ __launch_bounds__(kWaves * 64) void hot_dq_batch_kernel(const HotBatch m) {
+  const int g = xcd_item(blockIdx.x, m.first[m.n]);
+  const int r = batch_relation(m, g);
+  hot_dq_body<DP, BF>(m.rel[r], g - m.first[r]);
+}
+template <int DP, bool BF>
+__global__ __launch_bounds__(kWaves * 64) void hot_bwd_batch_kernel(const HotBatch m) {
+  const int g = xcd_item(blockIdx.x, m.first[m.n]);
+  const int r = batch_relation(m, g);
+  hot_bwd_body<DP, BF>(m.rel[r], g - m.first[r]);
 }
 
 bool hot_supported(int ds, int dt, bool same_dtype);
@@ -995,5 +1052,9 @@ hipError_t launch_row_prep(const RelArgs& a, int Tp, const unsigned char* tok_ok
 hipError_t launch_hot_fwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
 hipError_t launch_hot_dq(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
 hipError_t launch_hot_bwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
+// batch: the relations' first[] is filled by the launcher
+hipError_t launch_hot_fwd_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream);
+hipError_t launch_hot_dq_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream);
+hipError_t launch_hot_bwd_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream);
 
 }  // namespace lard

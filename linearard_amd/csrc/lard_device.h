@@ -70,6 +70,10 @@ struct RelArgs {
   //   dk_out = (scale_s * dk + dk_add) * (*dscale)
   const float* dk_add;  // [B, Hkv_s, T, Ds] or null (self relation: the row-side term dq)
   const float* dscale;  // device scalar or null (autograd's dloss)
+  // Throughput kernels only: device scalar or null, the relation's weight in
+  // a batched loss (multiplies the per-row KL, and the gradient wherever
+  // dscale is applied).
+  const float* weight;
 };
 
 // Outputs of the fused forward (one pass: both LSEs and the per-row KL).

@@ -70,6 +70,38 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert L.lard_attn_kl_backward_workspace_bytes(0, H, H, T, D, 0) == 0
 
 
+def test_batched_abi_rejects_bad_batches_without_a_gpu():
+    L = _lib.lib()
+    rels = (_lib.Relation * 2)()
+    for r in range(2):
+        for t in (rels[r].xs, rels[r].xt):
+            t.data = 256
+            t.size[:] = [1, 4 - 2 * r, 64, 128]
+            t.stride[:] = [t.size[1] * 64 * 128, 64 * 128, 128, 1]
+            t.dtype = 1
+        rels[r].lse_s = rels[r].lse_t = rels[r].dxs = 512
+    m = _lib.Mask()
+    ws = L.lard_attn_kl_batched_workspace_bytes(rels, 2)
+    # rows of both relations (KL terms, 256-aligned) + loss partials + validity bytes + two normalisers per row
+    rows = 1 * (4 + 2) * 64
+    assert ws == rows * 4 + 512 * 8 + 256 + 2 * rows * 4
+    assert L.lard_attn_kl_batched_workspace_bytes(None, 0) == 0
+    rc = L.lard_attn_kl_batched_forward(rels, 0, ctypes.byref(m), 1, 0.1, 0.1, None, 1024, None, 0, None)
+    assert rc == -1 and b"at least one relation" in L.lard_last_error()
+    rels[1].xs.size[2] = rels[1].xt.size[2] = 32  # another T
+    rc = L.lard_attn_kl_batched_forward(rels, 2, ctypes.byref(m), 1, 0.1, 0.1, None, 1024, None, 0, None)
+    assert rc == -1 and b"share B and T" in L.lard_last_error()
+    rels[1].xs.size[2] = rels[1].xt.size[2] = 64
+    rc = L.lard_attn_kl_batched_forward(rels, 2, ctypes.byref(m), 1, 3e-7, 0.1, None, 1024, None, 0, None)
+    assert rc == -2 and b"scales" in L.lard_last_error()
+    for r in range(2):
+        for t in (rels[r].xs, rels[r].xt):
+            t.size[3] = 256
+            t.stride[:] = [t.size[1] * 64 * 256, 64 * 256, 256, 1]
+    rc = L.lard_attn_kl_batched_backward(rels, 2, ctypes.byref(m), 1, 0.1, 0.1, None, None, None, 0, None)
+    assert rc == -2 and b"D <= 128" in L.lard_last_error()
+
+
 def test_python_wrappers_reject_cpu_tensors():
     from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
 
