@@ -178,8 +178,8 @@ def relation_kl_loss(qs, ks, vs, qt, kt, vt, attn_mask=None, sm_scale_s=None, sm
     xs, xt, w = [], [], []
     for layer in range(L):
         B, Hq, T, _ = qs[layer].shape
-        if attn_mask is None:
-            denom = torch.tensor(float(B * Hq * T), device=dev, dtype=torch.float32)
+        if attn_mask is None:  # a fill on the device: a host tensor here would be a synchronising copy
+            denom = torch.full((), float(B * Hq * T), device=dev, dtype=torch.float32)
         else:
             denom = attn_mask.sum().clamp_min(1).to(torch.float32) * Hq
         wl = 1.0 / (denom * max(1, L))
