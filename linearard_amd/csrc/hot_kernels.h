@@ -670,6 +670,9 @@ __device__ __forceinline__ void mfma_phase(const u16* t1, const unsigned* g1off,
   };
   ss = (f32x16)(0.f);
   st = (f32x16)(0.f);
+  // while this wave feeds the matrix unit it goes first; the other wave of
+  // the SIMD fills the gaps with its VALU phase
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int i = 0; i < PD && i < N; ++i) load(i);
 #pragma unroll
@@ -686,6 +689,7 @@ __device__ __forceinline__ void mfma_phase(const u16* t1, const unsigned* g1off,
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // ----------------------------------------------------------------------------
@@ -914,7 +918,9 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
         const int gsb = 2 * t + sb;
         if (causal && gsb < diag_sb) continue;
         f32x16 ss, st;
+        __builtin_amdgcn_s_setprio(1);  // the MFMA-feeding wave goes first (see mfma_phase)
         sub_scores<DP, BF>(lq[buf][0], 32 * sb, l32, half, fk_s, fk_t, ss, st);
+        __builtin_amdgcn_s_setprio(0);
         float dd[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
@@ -933,6 +939,7 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
             dd[r] = off + lim >= 0 ? dd[r] : 0.f;
           }
         }
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
           const u16x8 bop = pack_d<BF>(dd + 8 * m);  // D cast to the input dtype (kernel_C.py:233)
@@ -940,6 +947,7 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
           for (int db = 0; db < NDB; ++db)
             dk[db] = mfma32<BF>(tro.read(lq[buf][0], sb, m, db), bop, dk[db]);
         }
+        __builtin_amdgcn_s_setprio(0);
       }
     };
 
