@@ -501,9 +501,13 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
       __syncthreads();   // ... in every wave; this pair's buffers are free
       const int p4 = (k >> 1) + 3;
       if (p4 < ntiles) issue_tile(p4);
+      step(B, k >> 1, 1, A, (k >> 1) + 1, 0);
+      // the second tile one step later: all waves issuing their copies at
+      // once would stall on the full memory queue
       if (p4 + 1 < ntiles) issue_tile(p4 + 1);
+    } else {
+      step(B, k >> 1, 1, A, (k >> 1) + 1, 0);
     }
-    step(B, k >> 1, 1, A, (k >> 1) + 1, 0);
   }
 
   // merge the two halves of the row: common maxima, rescaled sums
@@ -628,6 +632,10 @@ __device__ __forceinline__ void free_run(int ntiles, MPhase mphase, VPhase vphas
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     mphase(2 * t);
+    // parts 1 and 2 of tile t+2, one phase after part 0: all waves issuing
+    // their copies at once would stall on the full memory queue
+    if (t >= 1 && t + 2 < ntiles)
+      for (int j = 1; j < 3; ++j) issue_part(t + 2, j);
     vphase(2 * t);
     mphase(2 * t + 1);
     vphase(2 * t + 1);
@@ -637,8 +645,7 @@ __device__ __forceinline__ void free_run(int ntiles, MPhase mphase, VPhase vphas
       else
         wait_vmcnt<0>();
       __syncthreads();
-      if (t + 3 < ntiles)
-        for (int j = 0; j < 3; ++j) issue_part(t + 3, j);
+      if (t + 3 < ntiles) issue_part(t + 3, 0);
     }
   }
   mphase(2 * ntiles);  // GEMM2 of the last sub-block
