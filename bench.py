@@ -26,6 +26,7 @@ copy of known size), else null.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg4]
     python bench.py --workload layers [--layers 4]   # batched relation loss vs the per-call loop
+    python bench.py --workload rope                  # RoPE pair producer, HBM roofline
 """
 
 from __future__ import annotations
@@ -217,6 +218,46 @@ def run_layers(args):
     }))
 
 
+def run_rope(args):
+    """The RoPE pair producer at the cfg4 shape (B=1, H=32, n=32768, d=128,
+    bf16; teacher base 1e4, student linear factor 8): one pass reads the
+    pre-RoPE x and writes both rotated tensors, HBM-bound."""
+    import torch
+
+    from linearard_amd.rope import rope_pair
+
+    B, H, n, d = 1, 32, 32768, 128
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((B, n, H, d), generator=g).to(torch.bfloat16).to(dev).permute(0, 2, 1, 3)  # [B,T,H,D] view
+    scaling = {"rope_type": "linear", "factor": 8.0}
+    for _ in range(args.warmup):
+        rope_pair(x, 1e4, scaling)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        rope_pair(x, 1e4, scaling)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps * 1e3
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = 3 * B * H * n * d * 2  # read x, write the two rotated tensors
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "RoPE teacher/student pair producer tokens/sec (one pass, both relations)",
+        "value": B * n / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "wall_ms_per_step": wall, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded Gaussian pre-RoPE [B,T,H,D] view)",
+        "config": {"workload": f"rope pair: B={B}, H={H}, n={n}, d={d}, linear factor 8", "B": B, "H": H, "n": n,
+                   "d": d},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": MI355X_HBM_GBPS, "unit": "GB/s",
+                     "frac": gbps / MI355X_HBM_GBPS, "traffic": None, "bytes_per_launch": nbytes},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -226,9 +267,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (counter-scale calibration)")
-    ap.add_argument("--workload", default="relation", choices=("relation", "layers"),
+    ap.add_argument("--workload", default="relation", choices=("relation", "layers", "rope"),
                     help="relation: one self relation at --config (the headline); layers: the train.py "
-                         "relation loss over --layers layers at cfg3 shapes, batched vs the per-call loop")
+                         "relation loss over --layers layers at cfg3 shapes, batched vs the per-call loop; "
+                         "rope: the RoPE pair producer at the cfg4 shape")
     ap.add_argument("--layers", type=int, default=4)
     args = ap.parse_args()
 
@@ -238,6 +280,9 @@ def main():
         sys.exit(2)
     if args.workload == "layers":
         run_layers(args)
+        return
+    if args.workload == "rope":
+        run_rope(args)
         return
 
     import torch

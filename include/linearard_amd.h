@@ -191,6 +191,25 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
                                   float sm_scale_s, float sm_scale_t, const float* weights, const float* dloss,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * RoPE pair producer -- the step before the path: each model's rotary
+ * embedding of the captured q / k (HF LLaMA apply_rotary_pos_emb, rotate_half
+ * layout), the teacher with its native frequencies and the student with the
+ * scaled ones of --student-rope-scaling (train.py:206-213; linear, factor 4
+ * or 8 in scripts/train_linearard_*.sh:9).  From the pre-RoPE x [B, H, T, D]
+ * (any element strides with stride[3] == 1, so a [B, T, H, D] tensor's
+ * permuted view needs no copy; D a multiple of 16) writes out_t and out_s,
+ * contiguous [B, H, T, D] of x's dtype:
+ *   out[i]       = R(R(x[i] c_i) + R(-x[i+D/2] s_i)),
+ *   out[i + D/2] = R(R(x[i+D/2] c_i) + R(x[i] s_i)),
+ * c_i, s_i = R(cos / sin of pos * inv_freq[i]) (the angle one float32
+ * product), R the rounding to x's dtype after every operation.
+ * inv_freq_t / inv_freq_s: device float32 [D/2]; position_ids: device int64
+ * [B, T] with batch stride pos_stride_b, or NULL for 0..T-1.
+ */
+int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s,
+                   const int64_t* position_ids, int64_t pos_stride_b, void* out_t, void* out_s, void* stream);
+
 /* Kernel ids of the timing hook. */
 #define LARD_KERNEL_FORWARD 0  /* one-pass forward: both LSEs and the per-row KL */
 #define LARD_KERNEL_ROW_GRAD 1 /* backward, row side: dq (kernel_C.py:224-239) */

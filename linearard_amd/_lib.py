@@ -89,6 +89,8 @@ SIGNATURES = {
     "lard_attn_kl_batched_backward": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
                                                      ctypes.c_float, _FP, _FP, ctypes.c_void_p, ctypes.c_size_t,
                                                      ctypes.c_void_p]),
+    "lard_rope_pair": (ctypes.c_int, [_T4P, _FP, _FP, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p]),
     "lard_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "lard_timing_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                         ctypes.POINTER(ctypes.c_int64)]),

@@ -47,8 +47,11 @@ def check_scale(value, default_dim: int, name: str) -> float:
     return float(value)
 
 
-def check_relations(qs, ks, qt, kt):
-    """The q/k preconditions of kernel_B.py:262-309 (no lse involved)."""
+def check_relations(qs, ks, qt, kt, strided_ok=False):
+    """The q/k preconditions of kernel_B.py:262-309 (no lse involved).  With
+    strided_ok (the batched caller API) any view with a unit last stride is
+    accepted -- e.g. the [B,T,H,D] projections of train.py:133-142 seen as
+    [B,H,T,D] -- and the library checks its alignment."""
     for t, n in ((qs, "qs"), (ks, "ks"), (qt, "qt"), (kt, "kt")):
         require(isinstance(t, torch.Tensor), f"{n} must be a torch.Tensor")
     require(qs.is_cuda and ks.is_cuda and qt.is_cuda and kt.is_cuda, "Q/K must be on CUDA")
@@ -66,8 +69,9 @@ def check_relations(qs, ks, qt, kt):
     require(qt.shape[0] == kt.shape[0], "qt/kt B must match")
     require(qt.shape[2] == kt.shape[2], "qt/kt T must match")
     require(qt.shape[3] == kt.shape[3], "qt/kt Dt must match")
-    require(qs.is_contiguous() and ks.is_contiguous(), "qs/ks must be contiguous")
-    require(qt.is_contiguous() and kt.is_contiguous(), "qt/kt must be contiguous")
+    if not strided_ok:
+        require(qs.is_contiguous() and ks.is_contiguous(), "qs/ks must be contiguous")
+        require(qt.is_contiguous() and kt.is_contiguous(), "qt/kt must be contiguous")
     require(qs.stride(-1) == 1 and ks.stride(-1) == 1, "qs/ks last-dim stride must be 1")
     require(qt.stride(-1) == 1 and kt.stride(-1) == 1, "qt/kt last-dim stride must be 1")
     B, Hq, T, Ds = qs.shape

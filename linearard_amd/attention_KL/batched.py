@@ -55,7 +55,7 @@ class AttnKLBatchedFn(torch.autograd.Function):
         dev = xs[0].device
         B, _, T, _ = xs[0].shape
         for r in range(n):
-            check_relations(xs[r], xs[r], xt[r], xt[r])
+            check_relations(xs[r], xs[r], xt[r], xt[r], strided_ok=True)
             require(xs[r].shape[0] == B and xs[r].shape[2] == T, "batched relations must share B and T")
         attn_mask = check_mask(attn_mask, dev, B, T)
         ss = [check_scale(sm_scale_s, x.shape[3], "sm_scale_s") for x in xs]
@@ -145,9 +145,12 @@ def attn_kl_align_batched(xs, xt, weights=None, attn_mask=None, causal=True, sm_
     """``sum_r weights[r] * attn_kl_align(xs[r], xs[r], xt[r], xt[r], ...)``.
 
     ``xs``, ``xt``: sequences of [B, H_r, T, D] student / teacher tensors
-    (one self relation each, as train.py:380-402 calls it); ``weights``: a
-    float32 tensor (or sequence) of one value per relation, default all 1.
-    Returns a 0-d float32 tensor; gradients flow to the ``xs`` tensors.
+    (one self relation each, as train.py:380-402 calls it), any views with a
+    unit last stride (the attention hook's [B, T, H, D] projections seen as
+    [B, H, T, D] need no .contiguous() copy, unlike train.py:133-142);
+    ``weights``: a float32 tensor (or sequence) of one value per relation,
+    default all 1.  Returns a 0-d float32 tensor; gradients flow to the
+    ``xs`` tensors.
     """
     xs, xt = list(xs), list(xt)
     require(len(xs) > 0 and len(xs) == len(xt), "xs and xt must hold the same number (>= 1) of relations")

@@ -18,6 +18,7 @@
 
 #include "../../include/linearard_amd.h"
 #include "hot_kernels.h"
+#include "rope_kernels.h"
 
 namespace {
 
@@ -786,4 +787,34 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
       return rc;
   }
   return ok();
+}
+
+int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s,
+                   const int64_t* position_ids, int64_t pos_stride_b, void* out_t, void* out_s, void* stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x")) != LARD_OK) return rc;
+  const int64_t B = x->size[0], H = x->size[1], T = x->size[2], D = x->size[3];
+  if (D % 16 != 0) return fail(LARD_ERR_UNSUPPORTED, "rope_pair needs D to be a multiple of 16");
+  if (B * H * T == 0) return ok();
+  if (inv_freq_t == nullptr || inv_freq_s == nullptr || out_t == nullptr || out_s == nullptr)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "inv_freq and outputs must not be NULL");
+  if (B * T * (D / 16) > (int64_t)INT32_MAX * 256)
+    return fail(LARD_ERR_UNSUPPORTED, "rope_pair grid too large");
+  lard::RopeArgs a{};
+  a.x = static_cast<const lard::u16*>(x->data);
+  a.sb = x->stride[0];
+  a.sh = x->stride[1];
+  a.st = x->stride[2];
+  a.B = (int)B;
+  a.H = (int)H;
+  a.T = (int)T;
+  a.D = (int)D;
+  a.inv_freq_t = inv_freq_t;
+  a.inv_freq_s = inv_freq_s;
+  a.pos = position_ids;
+  a.pos_sb = pos_stride_b;
+  a.out_t = static_cast<lard::u16*>(out_t);
+  a.out_s = static_cast<lard::u16*>(out_s);
+  return hip_status(lard::launch_rope_pair(a, x->dtype == LARD_DTYPE_BF16, static_cast<hipStream_t>(stream)),
+                    "rope_pair launch");
 }

@@ -157,3 +157,26 @@ def test_batched_is_deterministic(gpu_available):
     assert l1 == l2
     for x, y in zip(g1, g2):
         assert torch.equal(x, y)
+
+
+def test_batched_takes_the_hooks_strided_views(gpu_available):
+    """train.py:133-142 copies the captured [B, T, H, D] projections with
+    .contiguous(); the batched API reads the permuted views directly, with
+    the same results bit for bit."""
+    from linearard_amd.attention_KL import attn_kl_align_batched
+
+    g = torch.Generator(device="cuda").manual_seed(2)
+    bthd = [torch.randn((1, 96, H, 64), device="cuda", generator=g).to(torch.bfloat16) for H in (4, 2)]
+    bthd_t = [(x.float() + 0.3 * torch.randn(x.shape, device="cuda", generator=g)).to(torch.bfloat16) for x in bthd]
+    views = [x.permute(0, 2, 1, 3).detach().requires_grad_(True) for x in bthd]
+    copies = [x.permute(0, 2, 1, 3).contiguous().detach().requires_grad_(True) for x in bthd]
+    t_views = [x.permute(0, 2, 1, 3) for x in bthd_t]
+    assert not views[0].is_contiguous()
+    w = torch.tensor([0.5, 2.0], device="cuda")
+    l1 = attn_kl_align_batched(views, t_views, w)
+    l1.backward()
+    l2 = attn_kl_align_batched(copies, [x.contiguous() for x in t_views], w)
+    l2.backward()
+    assert l1.item() == l2.item()
+    for a, b in zip(views, copies):
+        assert torch.equal(a.grad, b.grad)
