@@ -102,6 +102,21 @@ def test_batched_abi_rejects_bad_batches_without_a_gpu():
     assert rc == -2 and b"D <= 128" in L.lard_last_error()
 
 
+def test_rope_abi_rejects_bad_arguments_without_a_gpu():
+    L = _lib.lib()
+    t = _lib.Tensor4()
+    t.data = 256
+    t.size[:] = [1, 2, 16, 8]
+    t.stride[:] = [256, 128, 8, 1]
+    t.dtype = 1
+    rc = L.lard_rope_pair(ctypes.byref(t), 512, 512, None, 0, 1024, 2048, None)
+    assert rc == -2 and b"multiple of 16" in L.lard_last_error()
+    t.size[3] = 64
+    t.stride[:] = [2048, 1024, 64, 1]
+    rc = L.lard_rope_pair(ctypes.byref(t), None, 512, None, 0, 1024, 2048, None)
+    assert rc == -1 and b"must not be NULL" in L.lard_last_error()
+
+
 def test_python_wrappers_reject_cpu_tensors():
     from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
 
