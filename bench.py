@@ -27,6 +27,7 @@ copy of known size), else null.
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg4]
     python bench.py --workload layers [--layers 4]   # batched relation loss vs the per-call loop
     python bench.py --workload rope                  # RoPE pair producer, HBM roofline
+    python bench.py --workload logits                # logits KL (train.py:412-420), HBM roofline
 """
 
 from __future__ import annotations
@@ -258,6 +259,103 @@ def run_rope(args):
     }))
 
 
+def run_logits(args):
+    """The logits KL of train.py:412-420 at the Llama-3-8B shape: B=1,
+    K=512 kept positions (--logits-keep-k, scripts/train_linearard_llama3.sh),
+    V=128256, bf16, T=1.  One step = forward (lard_logits_kl_forward) and
+    backward to the student logits (lard_logits_kl_backward), HBM-bound:
+    the forward reads both logits tensors once (4 bytes per vocabulary
+    entry), the gradient pass reads them again and writes the bf16 student
+    gradient (6 bytes per entry)."""
+    import numpy as np
+    import torch
+
+    from linearard_amd import _lib
+    from linearard_amd.logits_kl import logits_kl
+
+    B, K, V, T = 1, 512, 128256, 1.0
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    t = (3.0 * torch.randn((B, K, V), device=dev, generator=g)).to(torch.bfloat16)
+    s = (t.float() + 1.5 * torch.randn((B, K, V), device=dev, generator=g)).to(torch.bfloat16).requires_grad_(True)
+
+    def step():
+        s.grad = None
+        loss = logits_kl(t, s, temperature=T)
+        loss.backward()
+        return loss
+
+    L = _lib.lib()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _lib.check(L.lard_timing_enable(1), "lard_timing_enable")
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        loss = step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps * 1e3
+    _lib.check(L.lard_timing_enable(0), "lard_timing_enable")
+    ms = e0.elapsed_time(e1) / args.steps
+    kernel_ms = {}
+    for name in ("logits_forward", "logits_grad"):
+        total, count = ctypes.c_double(), ctypes.c_int64()
+        _lib.check(L.lard_timing_read(_lib.KERNEL_IDS[name], ctypes.byref(total), ctypes.byref(count)),
+                   "lard_timing_read")
+        if count.value:
+            kernel_ms[name] = total.value / count.value
+    elems = B * K * V
+    algo_bytes = {"logits_forward": 2 * elems * 2, "logits_grad": 3 * elems * 2}
+    gbps = {k: algo_bytes[k] / (v * 1e-3) / 1e9 for k, v in kernel_ms.items()}
+    dom = max(kernel_ms, key=kernel_ms.get)
+    summary = traffic_summary("logits")
+    traffic = None
+    if summary is not None and dom in summary.get("bytes_per_launch", {}):
+        traffic = summary["bytes_per_launch"][dom]
+    out = {
+        "metric": "logits-KL fwd+bwd kept-positions/sec (train.py:412-420)",
+        "value": B * K / (ms * 1e-3), "unit": "positions/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "wall_ms_per_step": wall, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian teacher logits, student = teacher + noise)",
+        "config": {"workload": f"logits KL: B={B}, K={K}, V={V} (Llama-3-8B), T={T}", "B": B, "K": K, "V": V,
+                   "temperature": T},
+        "kernel_ms": kernel_ms, "kernel_gbps": gbps,
+        "step_gbps": (algo_bytes["logits_forward"] + algo_bytes["logits_grad"]) / (ms * 1e-3) / 1e9,
+        "loss": float(loss.item()),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbps[dom], "peak": MI355X_HBM_GBPS, "unit": "GB/s",
+                     "frac": gbps[dom] / MI355X_HBM_GBPS, "traffic": traffic, "bytes_per_launch": algo_bytes[dom],
+                     "avg_launch_ms": kernel_ms[dom]},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import logits_kl as O
+
+        rows = 16
+        rng = np.random.default_rng(0)
+        tt = (3.0 * rng.standard_normal((1, rows, V))).astype(np.float32)
+        ss = (tt + 1.5 * rng.standard_normal((1, rows, V))).astype(np.float32)
+        reps, c0 = 0, time.perf_counter()
+        while True:
+            O.logits_kl(tt, ss, T, "bf16")
+            O.logits_kl_grads(tt, ss, T, "bf16")
+            reps += 1
+            if time.perf_counter() - c0 > 10.0:
+                break
+        dt = (time.perf_counter() - c0) / reps
+        out["cpu_baseline"] = {
+            "value": rows / dt, "unit": "positions/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} kept positions of V={V}, forward + both gradients, float64 numpy "
+                      f"(oracle.logits_kl), {reps} repetitions in {reps * dt:.1f} s; host "
+                      f"{platform.processor() or platform.machine()}",
+        }
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -267,10 +365,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (counter-scale calibration)")
-    ap.add_argument("--workload", default="relation", choices=("relation", "layers", "rope"),
+    ap.add_argument("--workload", default="relation", choices=("relation", "layers", "rope", "logits"),
                     help="relation: one self relation at --config (the headline); layers: the train.py "
                          "relation loss over --layers layers at cfg3 shapes, batched vs the per-call loop; "
-                         "rope: the RoPE pair producer at the cfg4 shape")
+                         "rope: the RoPE pair producer at the cfg4 shape; logits: the logits KL at the "
+                         "Llama-3-8B shape")
     ap.add_argument("--layers", type=int, default=4)
     args = ap.parse_args()
 
@@ -283,6 +382,9 @@ def main():
         return
     if args.workload == "rope":
         run_rope(args)
+        return
+    if args.workload == "logits":
+        run_logits(args)
         return
 
     import torch

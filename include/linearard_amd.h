@@ -39,6 +39,8 @@ extern "C" {
 /* element type of q / k (kernel_A.py:195-196 accepts fp16 and bf16 only) */
 #define LARD_DTYPE_F16 0
 #define LARD_DTYPE_BF16 1
+/* float32: logits only (lard_logits_kl_*) */
+#define LARD_DTYPE_F32 2
 
 /* attention-mask element type, [B, T], nonzero = valid token (kernel_A.py:218) */
 #define LARD_MASK_NONE 0
@@ -52,6 +54,14 @@ typedef struct lard_tensor4 {
   int64_t stride[4]; /* element strides, stride[3] == 1 */
   int32_t dtype;     /* LARD_DTYPE_* */
 } lard_tensor4;
+
+/* [B, K, V] logits of the K kept positions (logits_to_keep, train.py:343) */
+typedef struct lard_logits {
+  const void* data;  /* device pointer */
+  int64_t size[3];   /* B, K, V */
+  int64_t stride[3]; /* element strides, stride[2] == 1 */
+  int32_t dtype;     /* LARD_DTYPE_F16 / BF16 / F32 */
+} lard_logits;
 
 typedef struct lard_mask {
   const void* data;  /* device pointer, ignored when kind == LARD_MASK_NONE */
@@ -210,18 +220,58 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
 int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s,
                    const int64_t* position_ids, int64_t pos_stride_b, void* out_t, void* out_s, void* stream);
 
+/*
+ * Logits KL -- replaces the output-alignment lines of the distillation step
+ * (train.py:412-419):
+ *   t_logp = log_softmax(t_logits / T); s_logp = log_softmax(s_logits / T)
+ *   kl_per_tok = (t_logp.exp() * (t_logp - s_logp)).sum(-1); logits_kl = kl_per_tok.mean()
+ * over the [B, K, V] logits of the K kept positions (train.py:343-358).
+ * t_logits / s_logits: same shape and dtype (fp16, bf16 or fp32), V stride 1,
+ * rows on 16-byte boundaries (data 16-byte aligned, B and K strides multiples
+ * of 8 elements for 16-bit types, 4 for fp32).  The scaled logits are
+ * q = R(x * (1/T)) with 1/T a float32 quotient and R the rounding to the
+ * dtype (a tensor division by a host scalar); everything after that is
+ * float32.  Writes lse_t, lse_s (log-sum-exp of q) and kl_rows (KL of each
+ * kept position), float32 [B*K] contiguous, and the mean into *loss (NaN
+ * for B*K == 0, the mean of an empty tensor; rows of V == 0 give KL 0).
+ * Deterministic: fixed reduction orders.  workspace: at least
+ * lard_logits_kl_workspace_bytes(B*K, V) bytes, 16-byte aligned.
+ */
+size_t lard_logits_kl_workspace_bytes(int64_t rows, int64_t vocab);
+int lard_logits_kl_forward(const lard_logits* t_logits, const lard_logits* s_logits, float temperature,
+                           float* lse_t, float* lse_s, float* kl_rows, float* loss, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * Logits KL backward -- autograd of the same lines (train.py:424 backward):
+ *   grad_s = c (p_s - p_t) / T,  grad_t = c p_t (l_t - l_s - KL) / T
+ * with p_x = exp(q_x - lse_x), l_x = q_x - lse_x and c = dloss[r] * row_scale
+ * (dloss_per_row != 0: one upstream value per row, as for kl_per_tok) or
+ * dloss[0] * row_scale (the mean: row_scale = 1 / (B*K)).  grad_t / grad_s:
+ * [B, K, V] of the logits' dtype with the same layout rules, or NULL to skip
+ * (the reference's teacher runs under no_grad, train.py:337); written in the
+ * logits dtype (one rounding of the float32 value).  kl_rows is read only
+ * for grad_t.
+ */
+int lard_logits_kl_backward(const lard_logits* t_logits, const lard_logits* s_logits, float temperature,
+                            const float* lse_t, const float* lse_s, const float* kl_rows, const float* dloss,
+                            int dloss_per_row, float row_scale, const lard_logits* grad_t,
+                            const lard_logits* grad_s, void* stream);
+
 /* Kernel ids of the timing hook. */
 #define LARD_KERNEL_FORWARD 0  /* one-pass forward: both LSEs and the per-row KL */
 #define LARD_KERNEL_ROW_GRAD 1 /* backward, row side: dq (kernel_C.py:224-239) */
 #define LARD_KERNEL_COL_GRAD 2 /* backward, column side: dk (kernel_C.py:242-253) */
-#define LARD_KERNEL_COUNT 3
+#define LARD_KERNEL_LOGITS_FORWARD 3 /* logits KL forward pass (lard_logits_kl_forward) */
+#define LARD_KERNEL_LOGITS_GRAD 4    /* logits KL gradient pass (lard_logits_kl_backward) */
+#define LARD_KERNEL_COUNT 5
 
 /*
  * Timing hook for measurement harnesses -- no counterpart in the reference
  * (its kernels are timed from outside).  While enabled, every launch of the
- * three kernels above by lard_attn_kl_forward / lard_attn_kl_backward /
- * lard_kl_backward / lard_attn_kl_batched_* is bracketed by two HIP events
- * recorded on its launch stream.  lard_timing_read() waits for the recorded
+ * kernels above by lard_attn_kl_forward / lard_attn_kl_backward /
+ * lard_kl_backward / lard_attn_kl_batched_* / lard_logits_kl_* is bracketed
+ * by two HIP events recorded on its launch stream.  lard_timing_read() waits for the recorded
  * events and returns the summed elapsed milliseconds and the launch count of
  * one kernel since its last read, then clears them.  Off by default.  While enabled, launches
  * cannot be captured into a HIP graph and calls from several host threads

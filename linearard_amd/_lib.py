@@ -22,6 +22,7 @@ HEADER_PATH = os.path.join(os.path.dirname(PACKAGE_DIR), "include", "linearard_a
 LARD_OK = 0
 LARD_ERR_UNSUPPORTED = -2
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+LOGITS_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 MASK_CODES = {torch.bool: 1, torch.uint8: 1, torch.int32: 2, torch.int64: 3}
 
 
@@ -47,6 +48,17 @@ class Mask(ctypes.Structure):
     ]
 
 
+class Logits(ctypes.Structure):
+    """``lard_logits``: [B, K, V] logits of the kept positions."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("size", ctypes.c_int64 * 3),
+        ("stride", ctypes.c_int64 * 3),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 class Relation(ctypes.Structure):
     """``lard_relation``: one self relation of a batched loss."""
 
@@ -62,6 +74,7 @@ class Relation(ctypes.Structure):
 _T4P = ctypes.POINTER(Tensor4)
 _MP = ctypes.POINTER(Mask)
 _RP = ctypes.POINTER(Relation)
+_LP = ctypes.POINTER(Logits)
 _FP = ctypes.c_void_p  # float* device pointers are passed as addresses
 
 # name -> (restype, argtypes); must cover every function include/linearard_amd.h declares.
@@ -91,12 +104,17 @@ SIGNATURES = {
                                                      ctypes.c_void_p]),
     "lard_rope_pair": (ctypes.c_int, [_T4P, _FP, _FP, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                       ctypes.c_void_p, ctypes.c_void_p]),
+    "lard_logits_kl_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "lard_logits_kl_forward": (ctypes.c_int, [_LP, _LP, ctypes.c_float, _FP, _FP, _FP, _FP, ctypes.c_void_p,
+                                              ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_logits_kl_backward": (ctypes.c_int, [_LP, _LP, ctypes.c_float, _FP, _FP, _FP, _FP, ctypes.c_int,
+                                               ctypes.c_float, _LP, _LP, ctypes.c_void_p]),
     "lard_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "lard_timing_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                         ctypes.POINTER(ctypes.c_int64)]),
 }
 
-KERNEL_IDS = {"forward": 0, "row_grad": 1, "col_grad": 2}
+KERNEL_IDS = {"forward": 0, "row_grad": 1, "col_grad": 2, "logits_forward": 3, "logits_grad": 4}
 
 _LIB = None
 
@@ -139,6 +157,19 @@ def tensor4(t: torch.Tensor) -> Tensor4:
         d.size[i] = t.shape[i]
         d.stride[i] = t.stride(i)
     d.dtype = DTYPE_CODES[t.dtype]
+    return d
+
+
+def logits_desc(t: torch.Tensor) -> Logits:
+    """A [B, K, V] tensor (a [R, V] one is read as B = 1, K = R)."""
+    if t.ndim == 2:
+        t = t.unsqueeze(0)
+    d = Logits()
+    d.data = t.data_ptr()
+    for i in range(3):
+        d.size[i] = t.shape[i]
+        d.stride[i] = t.stride(i)
+    d.dtype = LOGITS_DTYPE_CODES[t.dtype]
     return d
 
 

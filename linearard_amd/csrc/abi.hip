@@ -18,6 +18,7 @@
 
 #include "../../include/linearard_amd.h"
 #include "hot_kernels.h"
+#include "logits_kl_kernels.h"
 #include "rope_kernels.h"
 
 namespace {
@@ -376,6 +377,73 @@ lard::HotArgs relation_args(const lard_relation& R, const lard_mask* mask, int c
   f.Tp = Tp;
   f.tok_ok = tok_ok;
   return f;
+}
+
+
+// ---- logits KL (lard_logits_kl_*) ----
+
+int logits_esize(int32_t dtype) { return dtype == LARD_DTYPE_F32 ? 4 : 2; }
+
+// [B, K, V] logits (or their gradient): vocabulary stride 1, 16-byte aligned
+// rows (the kernels read and write 16 bytes at a time).
+int check_logits(const lard_logits* x, const char* name) {
+  if (x == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
+  for (int i = 0; i < 3; ++i)
+    if (x->size[i] < 0) return fail(LARD_ERR_INVALID_ARGUMENT, "%s has a negative size", name);
+  if (x->dtype != LARD_DTYPE_F16 && x->dtype != LARD_DTYPE_BF16 && x->dtype != LARD_DTYPE_F32)
+    return fail(LARD_ERR_UNSUPPORTED, "%s dtype supports only fp16/bf16/fp32", name);
+  const int64_t n = x->size[0] * x->size[1] * x->size[2];
+  if (n == 0) return LARD_OK;
+  if (x->data == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "%s data pointer is NULL", name);
+  if (x->stride[2] != 1 && x->size[2] > 1)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "%s vocabulary stride must be 1", name);
+  const int64_t vec = 16 / logits_esize(x->dtype);
+  if (reinterpret_cast<uintptr_t>(x->data) % 16 != 0 || (x->size[0] > 1 && x->stride[0] % vec != 0) ||
+      (x->size[1] > 1 && x->stride[1] % vec != 0))
+    return fail(LARD_ERR_UNSUPPORTED, "%s rows must start on 16-byte boundaries", name);
+  return LARD_OK;
+}
+
+int check_logits_like(const lard_logits* x, const lard_logits* ref, const char* name) {
+  int rc;
+  if ((rc = check_logits(x, name)) != LARD_OK) return rc;
+  if (x->size[0] != ref->size[0] || x->size[1] != ref->size[1] || x->size[2] != ref->size[2])
+    return fail(LARD_ERR_INVALID_ARGUMENT, "%s shape must match the teacher logits", name);
+  if (x->dtype != ref->dtype) return fail(LARD_ERR_INVALID_ARGUMENT, "%s dtype must match the teacher logits", name);
+  return LARD_OK;
+}
+
+// 1 / T as a float32 quotient, as a tensor division by a host scalar forms it.
+int check_temperature(float temperature, float* inv) {
+  if (!std::isfinite(temperature) || temperature == 0.f)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "temperature must be finite and nonzero");
+  *inv = 1.0f / temperature;
+  if (!std::isfinite(*inv)) return fail(LARD_ERR_INVALID_ARGUMENT, "1 / temperature overflows float32");
+  return LARD_OK;
+}
+
+int logits_common(const lard_logits* t, const lard_logits* s, float temperature, lard::LogitsArgs* a) {
+  int rc;
+  if ((rc = check_logits(t, "t_logits")) != LARD_OK) return rc;
+  if ((rc = check_logits_like(s, t, "s_logits")) != LARD_OK) return rc;
+  *a = lard::LogitsArgs{};
+  if ((rc = check_temperature(temperature, &a->inv_temp)) != LARD_OK) return rc;
+  const int64_t rows = t->size[0] * t->size[1], V = t->size[2];
+  if (rows > INT32_MAX) return fail(LARD_ERR_UNSUPPORTED, "B * K must be < 2^31");
+  const lard::LogitsSplit sp = lard::logits_split(rows, V);
+  if (rows * sp.splits > INT32_MAX) return fail(LARD_ERR_UNSUPPORTED, "logits grid too large");
+  a->t = t->data;
+  a->s = s->data;
+  a->t_sb = t->stride[0];
+  a->t_sk = t->stride[1];
+  a->s_sb = s->stride[0];
+  a->s_sk = s->stride[1];
+  a->K = (int)(t->size[1] > 0 ? t->size[1] : 1);
+  a->rows = (int)rows;
+  a->V = V;
+  a->splits = sp.splits;
+  a->chunk = sp.chunk;
+  return LARD_OK;
 }
 
 }  // namespace
@@ -817,4 +885,74 @@ int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* 
   a.out_s = static_cast<lard::u16*>(out_s);
   return hip_status(lard::launch_rope_pair(a, x->dtype == LARD_DTYPE_BF16, static_cast<hipStream_t>(stream)),
                     "rope_pair launch");
+}
+
+size_t lard_logits_kl_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  return (size_t)rows * lard::logits_split(rows, vocab).splits * lard::kLogitsPartFloats * sizeof(float);
+}
+
+int lard_logits_kl_forward(const lard_logits* t_logits, const lard_logits* s_logits, float temperature,
+                           float* lse_t, float* lse_s, float* kl_rows, float* loss, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  int rc;
+  lard::LogitsArgs a;
+  if ((rc = logits_common(t_logits, s_logits, temperature, &a)) != LARD_OK) return rc;
+  if (loss == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "loss must not be NULL");
+  if (a.rows > 0 && (lse_t == nullptr || lse_s == nullptr || kl_rows == nullptr))
+    return fail(LARD_ERR_INVALID_ARGUMENT, "lse_t / lse_s / kl_rows must not be NULL");
+  const size_t need = lard_logits_kl_workspace_bytes(a.rows, a.V);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  a.part = static_cast<float*>(workspace);
+  a.lse_t = lse_t;
+  a.lse_s = lse_s;
+  a.kl = kl_rows;
+  a.loss = loss;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a.rows > 0 && a.V > 0) {
+    if ((rc = hip_status(timed(LARD_KERNEL_LOGITS_FORWARD, st,
+                               [&] { return lard::launch_logits_kl_forward(a, t_logits->dtype, st); }),
+                         "logits_kl forward launch")) != LARD_OK)
+      return rc;
+  }
+  return hip_status(lard::launch_logits_kl_finish(a, st), "logits_kl finish launch");
+}
+
+int lard_logits_kl_backward(const lard_logits* t_logits, const lard_logits* s_logits, float temperature,
+                            const float* lse_t, const float* lse_s, const float* kl_rows, const float* dloss,
+                            int dloss_per_row, float row_scale, const lard_logits* grad_t,
+                            const lard_logits* grad_s, void* stream) {
+  int rc;
+  lard::LogitsArgs a;
+  if ((rc = logits_common(t_logits, s_logits, temperature, &a)) != LARD_OK) return rc;
+  if (grad_t != nullptr && (rc = check_logits_like(grad_t, t_logits, "grad_t")) != LARD_OK) return rc;
+  if (grad_s != nullptr && (rc = check_logits_like(grad_s, t_logits, "grad_s")) != LARD_OK) return rc;
+  if (!std::isfinite(row_scale)) return fail(LARD_ERR_INVALID_ARGUMENT, "row_scale must be finite");
+  if (a.rows == 0 || a.V == 0 || (grad_t == nullptr && grad_s == nullptr)) return ok();
+  if (lse_t == nullptr || lse_s == nullptr || dloss == nullptr)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "lse_t / lse_s / dloss must not be NULL");
+  if (grad_t != nullptr && kl_rows == nullptr)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "kl_rows must not be NULL when grad_t is requested");
+  a.lse_t = const_cast<float*>(lse_t);
+  a.lse_s = const_cast<float*>(lse_s);
+  a.kl = const_cast<float*>(kl_rows);
+  a.dloss = dloss;
+  a.dloss_per_row = dloss_per_row != 0;
+  a.row_scale = row_scale;
+  if (grad_t != nullptr) {
+    a.gt = const_cast<void*>(grad_t->data);
+    a.gt_sb = grad_t->stride[0];
+    a.gt_sk = grad_t->stride[1];
+  }
+  if (grad_s != nullptr) {
+    a.gs = const_cast<void*>(grad_s->data);
+    a.gs_sb = grad_s->stride[0];
+    a.gs_sk = grad_s->stride[1];
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return hip_status(timed(LARD_KERNEL_LOGITS_GRAD, st, [&] { return lard::launch_logits_kl_grad(a, t_logits->dtype, st); }),
+                    "logits_kl backward launch");
 }

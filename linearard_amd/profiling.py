@@ -30,6 +30,8 @@ KERNEL_NAMES = {
     "fused_fwd_kernel": "forward",
     "hot_dq_kernel": "row_grad",
     "hot_bwd_kernel": "col_grad",
+    "logits_kl_forward_kernel": "logits_forward",
+    "logits_kl_grad_kernel": "logits_grad",
 }
 CALIBRATION_FRAGMENT = "neg_kernel"
 

@@ -117,6 +117,58 @@ def test_rope_abi_rejects_bad_arguments_without_a_gpu():
     assert rc == -1 and b"must not be NULL" in L.lard_last_error()
 
 
+def _logits_desc(B=1, K=4, V=64, dtype=1, data=4096):
+    d = _lib.Logits()
+    d.data = data
+    d.size[:] = [B, K, V]
+    d.stride[:] = [K * V, V, 1]
+    d.dtype = dtype
+    return d
+
+
+def test_logits_kl_abi_rejects_bad_arguments_without_a_gpu():
+    L = _lib.lib()
+    t, s = _logits_desc(), _logits_desc(data=8192)
+    f = [16384, 16384 + 64, 16384 + 128, 16384 + 192]  # lse_t, lse_s, kl, loss (never dereferenced)
+    ws = L.lard_logits_kl_workspace_bytes(4, 64)
+    assert ws >= 4 * 32 and L.lard_logits_kl_workspace_bytes(0, 64) == 0
+
+    def fwd(t, s, T=1.0, ws_bytes=ws, out=f):
+        return L.lard_logits_kl_forward(ctypes.byref(t) if t is not None else None, ctypes.byref(s), T, *out,
+                                        32768, ws_bytes, None)
+
+    assert fwd(None, s) == -1 and b"must not be NULL" in L.lard_last_error()
+    assert fwd(t, _logits_desc(V=32, data=8192)) == -1 and b"shape must match" in L.lard_last_error()
+    assert fwd(t, _logits_desc(dtype=0, data=8192)) == -1 and b"dtype must match" in L.lard_last_error()
+    assert fwd(_logits_desc(dtype=3), s) == -2 and b"fp16/bf16/fp32" in L.lard_last_error()
+    bad = _logits_desc()
+    bad.stride[2] = 2
+    assert fwd(bad, s) == -1 and b"vocabulary stride" in L.lard_last_error()
+    assert fwd(_logits_desc(data=4098), s) == -2 and b"16-byte" in L.lard_last_error()
+    odd = _logits_desc(V=63)
+    odd.stride[:] = [4 * 63, 63, 1]
+    assert fwd(odd, _logits_desc(V=63, data=8192)) == -2 and b"16-byte" in L.lard_last_error()
+    for T in (0.0, float("inf"), float("nan"), 1e-45):
+        assert fwd(t, s, T=T) == -1 and b"temperature" in L.lard_last_error()
+    assert fwd(t, s, ws_bytes=ws - 1) == -1 and b"workspace too small" in L.lard_last_error()
+    assert fwd(t, s, out=[f[0], f[1], f[2], None]) == -1 and b"loss" in L.lard_last_error()
+
+    g_bad = _logits_desc(dtype=2, data=65536)
+    rc = L.lard_logits_kl_backward(ctypes.byref(t), ctypes.byref(s), 1.0, f[0], f[1], f[2], f[3], 0, 0.25,
+                                   None, ctypes.byref(g_bad), None)
+    assert rc == -1 and b"grad_s dtype" in L.lard_last_error()
+    g = _logits_desc(data=65536)
+    rc = L.lard_logits_kl_backward(ctypes.byref(t), ctypes.byref(s), 1.0, f[0], f[1], None, f[3], 0, 0.25,
+                                   ctypes.byref(g), None, None)
+    assert rc == -1 and b"kl_rows" in L.lard_last_error()
+    rc = L.lard_logits_kl_backward(ctypes.byref(t), ctypes.byref(s), 1.0, f[0], f[1], f[2], None, 0, 0.25,
+                                   None, ctypes.byref(g), None)
+    assert rc == -1 and b"dloss" in L.lard_last_error()
+    # no gradient requested: nothing to do, no GPU call
+    assert L.lard_logits_kl_backward(ctypes.byref(t), ctypes.byref(s), 1.0, f[0], f[1], f[2], f[3], 0, 0.25,
+                                     None, None, None) == 0
+
+
 def test_python_wrappers_reject_cpu_tensors():
     from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
 
