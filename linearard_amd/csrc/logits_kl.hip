@@ -40,8 +40,7 @@ constexpr float kStartMax = -1e30f;   // running maximum (base-2 units) before t
 constexpr float kPadLogit = -3e38f;   // logits past V: exp2 underflows to 0 and q_t - q_s = 0
 constexpr float kLazyGroupSum = 1048576.f;
 constexpr int kThreads = 256;
-constexpr int64_t kStep = kThreads * 8;  // logits per workgroup per group
-constexpr int kUnroll = 4;
+constexpr int64_t kStep = kThreads * 8;  // logits per workgroup per group of 8
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
@@ -50,15 +49,16 @@ struct Raw {
   u32x4 w[DT == kLogitsF32 ? 2 : 1];
 };
 
+// Streaming (nontemporal) loads: every logit is read once per pass.
 template <int DT>
 __device__ __forceinline__ Raw<DT> load_raw(const void* row, int64_t v) {
   Raw<DT> r;
   if constexpr (DT == kLogitsF32) {
     const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(row) + v);
-    r.w[0] = p[0];
-    r.w[1] = p[1];
+    r.w[0] = __builtin_nontemporal_load(p);
+    r.w[1] = __builtin_nontemporal_load(p + 1);
   } else {
-    r.w[0] = *reinterpret_cast<const u32x4*>(static_cast<const u16*>(row) + v);
+    r.w[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const u16*>(row) + v));
   }
   return r;
 }
@@ -143,7 +143,7 @@ __device__ __forceinline__ void store8(void* row, int64_t v, int64_t v1, const f
       for (int j = 0; j < 4; ++j)
         w[j] = (unsigned)to_bits(g[2 * j], DT == kLogitsBF16) |
                ((unsigned)to_bits(g[2 * j + 1], DT == kLogitsBF16) << 16);
-      *reinterpret_cast<u32x4*>(static_cast<u16*>(row) + v) = w;
+      *reinterpret_cast<u32x4*>(static_cast<u16*>(row) + v) = w;  // plain stores measured faster than nt
     }
   } else {
 #pragma unroll
@@ -269,38 +269,86 @@ __device__ __forceinline__ RowSpan row_span(const LogitsArgs& a) {
   return r;
 }
 
+
+// Groups of 8 per thread in one unit: 16 bytes of each row per group for
+// 16-bit types (2 groups), 32 bytes for fp32 (1 group): 4096 logits per
+// workgroup, 64 bytes of loads per thread in flight during the compute.
+// (62 VGPRs: 8 waves per SIMD; 4 groups per unit measured slower.)
+template <int DT>
+constexpr int kGroups = DT == kLogitsF32 ? 1 : 2;
+
+template <int DT>
+struct Unit {
+  Raw<DT> t[kGroups<DT>], s[kGroups<DT>];
+};
+
+// Loads every group of a unit.  Groups that do not lie wholly inside the
+// chunk load the row's first 8 logits instead (V >= 8) and are never
+// visited: the loads stay unconditional, so the compiler's wait counts stay
+// exact and the next unit's loads remain in flight during the compute.
+template <int DT>
+__device__ __forceinline__ void load_unit(Unit<DT>& u, const RowSpan& r, int64_t v) {
+#pragma unroll
+  for (int g = 0; g < kGroups<DT>; ++g) {
+    const int64_t gv = v + g * kStep;
+    const int64_t src = gv + 8 <= r.v1 ? gv : 0;
+    u.t[g] = load_raw<DT>(r.t, src);
+    u.s[g] = load_raw<DT>(r.s, src);
+  }
+}
+
+template <int DT, bool SCALED, class F>
+__device__ __forceinline__ void visit_unit(const Unit<DT>& u, const RowSpan& r, int64_t v, float inv_temp, F& f) {
+#pragma unroll
+  for (int g = 0; g < kGroups<DT>; ++g) {
+    const int64_t gv = v + g * kStep;
+    if (gv + 8 <= r.v1) {
+      float t[8], s[8];
+      unpack<DT, SCALED>(u.t[g], inv_temp, t);
+      unpack<DT, SCALED>(u.s[g], inv_temp, s);
+      f(gv, t, s, true);
+    }
+  }
+}
+
+// Streams this thread's groups of 8 logits of the chunk through
+// f(v, t, s, full), one unit at a time, with the next unit's loads in flight
+// while the current one is computed (two register buffers, no copies).  The
+// group holding the row's last V % 8 logits (all of them when V < 8) is
+// read element by element after the loop, padded with `pad`, and passed
+// with full = false.
+template <int DT, bool SCALED, class F>
+__device__ __forceinline__ void stream_chunk(const RowSpan& r, int64_t V, float inv_temp, float pad, F& f) {
+  constexpr int64_t kUnitStep = kGroups<DT> * kStep;
+  if (V >= 8) {
+    int64_t v = r.v0 + threadIdx.x * 8;
+    Unit<DT> a, b;
+    load_unit<DT>(a, r, v);
+    while (v < r.v1) {
+      load_unit<DT>(b, r, v + kUnitStep);
+      visit_unit<DT, SCALED>(a, r, v, inv_temp, f);
+      v += kUnitStep;
+      if (v >= r.v1) break;
+      load_unit<DT>(a, r, v + kUnitStep);
+      visit_unit<DT, SCALED>(b, r, v, inv_temp, f);
+      v += kUnitStep;
+    }
+  }
+  const int64_t gp = V & ~(int64_t)7;
+  if (gp < V && gp >= r.v0 && gp < r.v1 && (int)(((gp - r.v0) >> 3) % kThreads) == (int)threadIdx.x) {
+    float t[8], s[8];
+    load_tail<DT, SCALED>(r.t, gp, r.v1, inv_temp, pad, t);
+    load_tail<DT, SCALED>(r.s, gp, r.v1, inv_temp, pad, s);
+    f(gp, t, s, false);
+  }
+}
+
 template <int DT, bool SCALED>
 __global__ __launch_bounds__(kThreads) void logits_kl_forward_kernel(const LogitsArgs a) {
   const RowSpan r = row_span<DT>(a);
   Acc c{kStartMax, 0.f, 0.f, kStartMax, 0.f};
-  int64_t v = r.v0 + threadIdx.x * 8;
-  // full iterations: all kUnroll groups of this thread end inside the chunk
-  for (; v + (kUnroll - 1) * kStep + 8 <= r.v1; v += kUnroll * kStep) {
-    Raw<DT> rt[kUnroll], rs[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      rt[u] = load_raw<DT>(r.t, v + u * kStep);
-      rs[u] = load_raw<DT>(r.s, v + u * kStep);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float t[8], s[8];
-      unpack<DT, SCALED>(rt[u], a.inv_temp, t);
-      unpack<DT, SCALED>(rs[u], a.inv_temp, s);
-      add_group(c, t, s);
-    }
-  }
-  for (; v < r.v1; v += kStep) {
-    float t[8], s[8];
-    if (v + 8 <= r.v1) {
-      unpack<DT, SCALED>(load_raw<DT>(r.t, v), a.inv_temp, t);
-      unpack<DT, SCALED>(load_raw<DT>(r.s, v), a.inv_temp, s);
-    } else {
-      load_tail<DT, SCALED>(r.t, v, r.v1, a.inv_temp, kPadLogit, t);
-      load_tail<DT, SCALED>(r.s, v, r.v1, a.inv_temp, kPadLogit, s);
-    }
-    add_group(c, t, s);
-  }
+  auto f = [&](int64_t, const float (&t)[8], const float (&s)[8], bool) { add_group(c, t, s); };
+  stream_chunk<DT, SCALED>(r, a.V, a.inv_temp, kPadLogit, f);
   const Acc m = block_merge(c);
   if (threadIdx.x == 0) {
     float* p = a.part + ((int64_t)r.row * a.splits + (int)(blockIdx.x % (unsigned)a.splits)) * kLogitsPartFloats;
@@ -365,7 +413,7 @@ __global__ __launch_bounds__(kThreads) void logits_kl_grad_kernel(const LogitsAr
   const float lt2 = lt * kL2E, ls2 = ls * kL2E;
   const float kl = GT ? a.kl[r.row] : 0.f;
 
-  auto group = [&](int64_t v, const float (&t)[8], const float (&s)[8]) {
+  auto group = [&](int64_t v, const float (&t)[8], const float (&s)[8], bool full) {
     float g_s[8], g_t[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -374,37 +422,11 @@ __global__ __launch_bounds__(kThreads) void logits_kl_grad_kernel(const LogitsAr
       g_s[e] = c * (ps - pt);
       g_t[e] = c * pt * ((t[e] - lt) - (s[e] - ls) - kl);
     }
-    if constexpr (GS) store8<DT>(gs, v, r.v1, g_s);
-    if constexpr (GT) store8<DT>(gt, v, r.v1, g_t);
+    if constexpr (GS) store8<DT>(gs, v, full ? v + 8 : r.v1, g_s);
+    if constexpr (GT) store8<DT>(gt, v, full ? v + 8 : r.v1, g_t);
   };
 
-  int64_t v = r.v0 + threadIdx.x * 8;
-  for (; v + (kUnroll - 1) * kStep + 8 <= r.v1; v += kUnroll * kStep) {
-    Raw<DT> rt[kUnroll], rs[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      rt[u] = load_raw<DT>(r.t, v + u * kStep);
-      rs[u] = load_raw<DT>(r.s, v + u * kStep);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float t[8], s[8];
-      unpack<DT, SCALED>(rt[u], a.inv_temp, t);
-      unpack<DT, SCALED>(rs[u], a.inv_temp, s);
-      group(v + u * kStep, t, s);
-    }
-  }
-  for (; v < r.v1; v += kStep) {
-    float t[8], s[8];
-    if (v + 8 <= r.v1) {
-      unpack<DT, SCALED>(load_raw<DT>(r.t, v), a.inv_temp, t);
-      unpack<DT, SCALED>(load_raw<DT>(r.s, v), a.inv_temp, s);
-    } else {  // pad values are never stored (store8 stops at v1)
-      load_tail<DT, SCALED>(r.t, v, r.v1, a.inv_temp, 0.f, t);
-      load_tail<DT, SCALED>(r.s, v, r.v1, a.inv_temp, 0.f, s);
-    }
-    group(v, t, s);
-  }
+  stream_chunk<DT, SCALED>(r, a.V, a.inv_temp, 0.f, group);  // pad values are never stored (store8 stops at v1)
 }
 
 template <int DT, bool SCALED>

@@ -9,25 +9,28 @@ namespace lard {
 enum LogitsDtype { kLogitsF16 = 0, kLogitsBF16 = 1, kLogitsF32 = 2 };
 
 // Vocabulary split: a row of V logits is cut into `splits` chunks of
-// `chunk` elements (a multiple of 8), one workgroup each.
+// `chunk` elements, one workgroup each.  Chunks are whole multiples of
+// kLogitsUnit logits (two of the kernels' load steps of 4096 logits).
+constexpr int64_t kLogitsUnit = 8192;
+#ifndef LARD_LOGITS_TARGET_BLOCKS
+#define LARD_LOGITS_TARGET_BLOCKS 2048
+#endif
+
 struct LogitsSplit {
   int splits;
   int64_t chunk;
 };
 
-// Splits chosen so the grid has about 2048 workgroups (8 per CU) and every
-// chunk holds at least 8192 logits (4 groups of 8 per thread).
+// Splits chosen so the grid has about LARD_LOGITS_TARGET_BLOCKS workgroups
+// (at most one per unit, at most 64 per row).
 inline LogitsSplit logits_split(int64_t rows, int64_t V) {
-  int64_t by_blocks = rows > 0 ? (2048 + rows - 1) / rows : 1;
-  int64_t by_size = V / 8192;
-  int64_t s = by_blocks < by_size ? by_blocks : by_size;
-  if (s < 1) s = 1;
+  const int64_t units = V > 0 ? (V + kLogitsUnit - 1) / kLogitsUnit : 1;
+  int64_t s = rows > 0 ? (LARD_LOGITS_TARGET_BLOCKS + rows - 1) / rows : 1;
+  if (s > units) s = units;
   if (s > 64) s = 64;
-  int64_t chunk = (V + s - 1) / s;
-  chunk = (chunk + 7) / 8 * 8;
-  if (chunk < 8) chunk = 8;
-  s = (V + chunk - 1) / chunk;
   if (s < 1) s = 1;
+  const int64_t chunk = (units + s - 1) / s * kLogitsUnit;
+  s = V > 0 ? (V + chunk - 1) / chunk : 1;
   return {(int)s, chunk};
 }
 

@@ -273,11 +273,14 @@ def test_kept_positions_as_a_strided_view(gpu_available):
 def test_edge_cases(gpu_available):
     from linearard_amd.logits_kl import logits_kl
 
-    one = torch.randn((2, 3, 1), device="cuda").to(torch.bfloat16)
-    xs = torch.randn((2, 3, 1), device="cuda").to(torch.bfloat16).requires_grad_(True)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    one = (4.0 * torch.randn((2, 3, 1), device="cuda", generator=g)).to(torch.bfloat16)
+    xs = (4.0 * torch.randn((2, 3, 1), device="cuda", generator=g)).to(torch.bfloat16).requires_grad_(True)
     loss = logits_kl(one, xs)
     loss.backward()
-    assert loss.item() == 0.0 and bool((xs.grad == 0).all())  # one word: both distributions are 1
+    # one word: both distributions are 1 and the KL 0, up to the float32
+    # roundings of KL = E[q_t - q_s] - lse_t + lse_s (|q| <= 16 here)
+    assert abs(loss.item()) <= 1e-5 and float(xs.grad.float().abs().max()) <= 1e-6
     empty = torch.empty((1, 0, 100), device="cuda", dtype=torch.bfloat16)
     assert math.isnan(logits_kl(empty, empty).item())  # the mean of no positions, as torch gives
     novocab = torch.empty((1, 4, 0), device="cuda", dtype=torch.bfloat16)
