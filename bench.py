@@ -28,6 +28,7 @@ copy of known size), else null.
     python bench.py --workload layers [--layers 4]   # batched relation loss vs the per-call loop
     python bench.py --workload rope                  # RoPE pair producer, HBM roofline
     python bench.py --workload logits                # logits KL (train.py:412-420), HBM roofline
+    python bench.py --workload step --steps 2 --warmup 1   # cfg5 distillation-step loss (32 layers)
 """
 
 from __future__ import annotations
@@ -382,6 +383,104 @@ def run_logits(args):
     print(json.dumps(out))
 
 
+def run_step(args):
+    """The loss side of one distillation step at SURVEY cfg5 (train.py:323-424
+    for a Mistral-7B-v0.1-shaped model): 32 layers x (Q/Q 32 heads, K/K 8,
+    V/V 8), B=2, n=16384, d=128, causal, all-ones PG19 mask; teacher RoPE
+    base 1e4 at positions p, student linear interpolation x4; kept-position
+    logits [2, 512, 32000]; lam_A = 1, lam_L = 0, T = 1 (the scripts'
+    values).  One step = the RoPE pairs of every layer's q and k
+    (rope_pair), distillation_loss (batched relation launches + logits KL)
+    and its backward to the student tensors.  Pre-RoPE activations are
+    Gaussian with a Student-t(3) subset of 8 channels; the student's v is the
+    teacher's plus 0.1 N(0,1)."""
+    import torch
+
+    from linearard_amd.distill import distillation_loss
+    from linearard_amd.rope import rope_pair as rope
+
+    Lyr, B, n, Hq, Hkv, d, Kkeep, vocab = args.layers_step, 2, 16384, 32, 8, 128, 512, 32000
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    heavy = torch.arange(0, d, d // 8, device=dev)  # 8 heavy-tailed channels
+
+    def draw(H):
+        """[B, T, H, D] activations (the attention hook's layout), bf16."""
+        x = torch.randn((B, n, H, d), device=dev, generator=g)
+        z = torch.randn((B, n, H, heavy.numel()), device=dev, generator=g)
+        chi = torch.randn((B, n, H, heavy.numel(), 3), device=dev, generator=g).pow(2).sum(-1)
+        x[..., heavy] = z / torch.sqrt(chi / 3.0)
+        return x.to(torch.bfloat16)
+
+    q_pre = [draw(Hq).permute(0, 2, 1, 3) for _ in range(Lyr)]
+    k_pre = [draw(Hkv).permute(0, 2, 1, 3) for _ in range(Lyr)]
+    v_t = [draw(Hkv).permute(0, 2, 1, 3) for _ in range(Lyr)]
+    v_s = [(v.float() + 0.1 * torch.randn(v.shape, device=dev, generator=g)).to(torch.bfloat16) for v in v_t]
+    mask = torch.ones((B, n), device=dev, dtype=torch.int64)
+    t_logits = (3.0 * torch.randn((B, Kkeep, vocab), device=dev, generator=g)).to(torch.bfloat16)
+    s_logits = (t_logits.float() + torch.randn(t_logits.shape, device=dev, generator=g)).to(torch.bfloat16)
+    scaling = {"rope_type": "linear", "factor": 4.0}
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record(stream)
+        qs, qt, ks, kt = [], [], [], []
+        for l in range(Lyr):
+            a, b = rope(q_pre[l], 1e4, scaling)
+            qs.append(a.requires_grad_(True))
+            qt.append(b)
+            a, b = rope(k_pre[l], 1e4, scaling)
+            ks.append(a.requires_grad_(True))
+            kt.append(b)
+        vs = [v.detach().requires_grad_(True) for v in v_s]
+        ev[1].record(stream)
+        out = distillation_loss(qs, ks, vs, qt, kt, v_t, t_logits, s_logits, attn_mask=mask,
+                                lam_A=1.0, lam_L=0.0, temperature=1.0)
+        ev[2].record(stream)
+        out.loss.backward()
+        ev[3].record(stream)
+        return out, ev
+
+    base_mem = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    res = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out, ev = step()
+        res.append(ev)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps * 1e3
+    peak = torch.cuda.max_memory_allocated(dev) - base_mem
+    phase = {"rope_pairs": 0.0, "loss_forward": 0.0, "backward": 0.0}
+    for ev in res:
+        phase["rope_pairs"] += ev[0].elapsed_time(ev[1]) / args.steps
+        phase["loss_forward"] += ev[1].elapsed_time(ev[2]) / args.steps
+        phase["backward"] += ev[2].elapsed_time(ev[3]) / args.steps
+    ms = sum(ev[0].elapsed_time(ev[3]) for ev in res) / args.steps
+    rel_tokens = Lyr * B * n * (Hq + 2 * Hkv)
+    flops = Lyr * (algorithmic_flops(B, Hq, n, d) + 2 * algorithmic_flops(B, Hkv, n, d))
+    print(json.dumps({
+        "metric": "distillation-step loss fwd+bwd relation-tokens/sec at cfg5 (train.py:360-424)",
+        "value": rel_tokens / (ms * 1e-3), "unit": "relation-tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "wall_ms_per_step": wall, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian activations with 8 Student-t(3) channels; RoPE teacher at p, "
+                "student at p/4; logits teacher + noise)",
+        "config": {"workload": f"cfg5 step: {Lyr} layers x (Q/Q {Hq} heads, K/K {Hkv}, V/V {Hkv}), B={B}, n={n}, "
+                               f"d={d}, causal, all-ones mask; logits [{B}, {Kkeep}, {vocab}], lam_A=1, lam_L=0",
+                   "layers": Lyr, "B": B, "n": n, "d": d, "Hq": Hq, "Hkv": Hkv},
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS,
+        "flop_per_step": flops, "phase_ms": phase, "peak_hbm_bytes": int(peak),
+        "losses": {k: float(v.detach()) for k, v in out._asdict().items()},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -391,11 +490,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (counter-scale calibration)")
-    ap.add_argument("--workload", default="relation", choices=("relation", "layers", "rope", "logits"),
+    ap.add_argument("--workload", default="relation", choices=("relation", "layers", "rope", "logits", "step"),
                     help="relation: one self relation at --config (the headline); layers: the train.py "
                          "relation loss over --layers layers at cfg3 shapes, batched vs the per-call loop; "
                          "rope: the RoPE pair producer at the cfg4 shape; logits: the logits KL at the "
-                         "Llama-3-8B shape")
+                         "Llama-3-8B shape; step: the loss side of a cfg5 distillation step")
+    ap.add_argument("--layers-step", type=int, default=32, help="layers of the step workload (cfg5: 32)")
     ap.add_argument("--layers", type=int, default=4)
     args = ap.parse_args()
 
@@ -411,6 +511,9 @@ def main():
         return
     if args.workload == "logits":
         run_logits(args)
+        return
+    if args.workload == "step":
+        run_step(args)
         return
 
     import torch

@@ -169,6 +169,18 @@ def test_logits_kl_abi_rejects_bad_arguments_without_a_gpu():
                                      None, None, None) == 0
 
 
+def test_distillation_loss_validates_its_lists_without_a_gpu():
+    from linearard_amd.distill import distillation_loss
+
+    x = torch.zeros((1, 2, 8, 16), dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="one tensor per layer"):
+        distillation_loss([x, x], [x], [x], [x], [x], [x])
+    with pytest.raises(AssertionError, match="one tensor per layer"):
+        distillation_loss([], [], [], [], [], [])
+    with pytest.raises(AssertionError, match="given together"):
+        distillation_loss([x], [x], [x], [x], [x], [x], t_logits=torch.zeros((1, 2, 4)))
+
+
 def test_python_wrappers_reject_cpu_tensors():
     from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
 
