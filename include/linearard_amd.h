@@ -12,7 +12,8 @@
  *     passed in by the caller, sized by the matching *_workspace_bytes().
  *   - q/k tensors are [B, H, T, D] with element strides; stride[3] must be 1,
  *     the data pointer 16-byte aligned and strides[0..2] multiples of 8
- *     (every contiguous tensor with D in {8,16,32,64,128,256} qualifies).
+ *     elements (4 for float32; every contiguous tensor with D in
+ *     {8,16,32,64,128,256} qualifies).
  *   - Outputs (lse, dq, dk, dx) are contiguous float32 of the stated shape.
  *   - GQA: kv head of query head h is h / (Hq / Hkv)   (kernel_A.py:77).
  *   - All work is enqueued on `stream` (a hipStream_t) and is asynchronous;
@@ -39,7 +40,10 @@ extern "C" {
 /* element type of q / k (kernel_A.py:195-196 accepts fp16 and bf16 only) */
 #define LARD_DTYPE_F16 0
 #define LARD_DTYPE_BF16 1
-/* float32: logits only (lard_logits_kl_*) */
+/* float32 (an extension): q / k of the stage and single-relation entry points
+ * (float32 products, D not rounded; both sides float32, strides multiples of
+ * 4 elements), and logits (lard_logits_kl_*).  The batched relation entry
+ * points and lard_rope_pair take fp16/bf16 only. */
 #define LARD_DTYPE_F32 2
 
 /* attention-mask element type, [B, T], nonzero = valid token (kernel_A.py:218) */

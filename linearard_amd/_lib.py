@@ -21,7 +21,7 @@ HEADER_PATH = os.path.join(os.path.dirname(PACKAGE_DIR), "include", "linearard_a
 
 LARD_OK = 0
 LARD_ERR_UNSUPPORTED = -2
-DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 LOGITS_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 MASK_CODES = {torch.bool: 1, torch.uint8: 1, torch.int32: 2, torch.int64: 3}
 

@@ -13,7 +13,9 @@ import torch
 
 SUPPORTED_HEAD_DIMS = (8, 16, 32, 64, 128, 256)  # kernel_A.py:18
 
-_HALF_TYPES = (torch.float16, torch.bfloat16)
+# fp16 / bf16 as the reference (kernel_A.py:195-196), plus float32 (the
+# library's float32 stage kernels; both sides must then be float32)
+_INPUT_TYPES = (torch.float16, torch.bfloat16, torch.float32)
 _MASK_TYPES = (torch.bool, torch.int32, torch.int64, torch.uint8)
 
 
@@ -55,10 +57,12 @@ def check_relations(qs, ks, qt, kt, strided_ok=False):
     for t, n in ((qs, "qs"), (ks, "ks"), (qt, "qt"), (kt, "kt")):
         require(isinstance(t, torch.Tensor), f"{n} must be a torch.Tensor")
     require(qs.is_cuda and ks.is_cuda and qt.is_cuda and kt.is_cuda, "Q/K must be on CUDA")
-    require(qs.dtype in _HALF_TYPES, "qs dtype supports only fp16/bf16")
-    require(ks.dtype in _HALF_TYPES, "ks dtype supports only fp16/bf16")
-    require(qt.dtype in _HALF_TYPES, "qt dtype supports only fp16/bf16")
-    require(kt.dtype in _HALF_TYPES, "kt dtype supports only fp16/bf16")
+    require(qs.dtype in _INPUT_TYPES, "qs dtype supports only fp16/bf16/fp32")
+    require(ks.dtype in _INPUT_TYPES, "ks dtype supports only fp16/bf16/fp32")
+    require(qt.dtype in _INPUT_TYPES, "qt dtype supports only fp16/bf16/fp32")
+    require(kt.dtype in _INPUT_TYPES, "kt dtype supports only fp16/bf16/fp32")
+    require((qs.dtype == torch.float32) == (qt.dtype == torch.float32),
+            "float32 inputs need float32 on both sides")
     require(qs.dtype == ks.dtype, "qs/ks dtype must match")
     require(qt.dtype == kt.dtype, "qt/kt dtype must match")
     require(qs.ndim == 4 and ks.ndim == 4, "qs/ks shape must be [B,H,T,Ds]")

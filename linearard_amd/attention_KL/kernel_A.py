@@ -1,7 +1,8 @@
 """Stage A: per-row log-sum-exp of one relation (mirrors kernel_A.py:190-265).
 
 ``lse_stats(q, k, attn_mask=None, causal=True, sm_scale=None)`` takes
-q [B,Hq,T,D] and k [B,Hkv,T,D] (fp16/bf16, contiguous, on the GPU) and
+q [B,Hq,T,D] and k [B,Hkv,T,D] (fp16/bf16 as the reference, or float32;
+contiguous, on the GPU) and
 returns lse [B,Hq,T] float32: log sum_j exp(sm_scale * q_i . k_j) over the
 valid set (padding mask, causal), 0 for masked rows.  The work runs in
 ``lard_lse_stats`` of liblinearard_amd.so.
@@ -24,8 +25,8 @@ def lse_stats(q, k, attn_mask=None, causal=True, sm_scale=None):
     require(isinstance(q, torch.Tensor), "q must be a torch.Tensor")
     require(isinstance(k, torch.Tensor), "k must be a torch.Tensor")
     require(q.is_cuda and k.is_cuda, "q/k must be on CUDA")
-    require(q.dtype in (torch.float16, torch.bfloat16), "q dtype supports only fp16/bf16")
-    require(k.dtype in (torch.float16, torch.bfloat16), "k dtype supports only fp16/bf16")
+    require(q.dtype in (torch.float16, torch.bfloat16, torch.float32), "q dtype supports only fp16/bf16/fp32")
+    require(k.dtype in (torch.float16, torch.bfloat16, torch.float32), "k dtype supports only fp16/bf16/fp32")
     require(q.dtype == k.dtype, "q/k dtype must match")
     require(q.ndim == 4 and k.ndim == 4, "q/k shape must be [B,H,T,D]")
     require(q.shape[0] == k.shape[0], "q/k B must match")

@@ -20,6 +20,7 @@
 #include "hot_kernels.h"
 #include "logits_kl_kernels.h"
 #include "rope_kernels.h"
+#include "stage_f32.h"
 
 namespace {
 
@@ -58,12 +59,13 @@ int check_tensor(const lard_tensor4* t, const char* name) {
     return fail(LARD_ERR_INVALID_ARGUMENT, "%s data pointer is NULL", name);
   for (int i = 0; i < 4; ++i)
     if (t->size[i] < 0) return fail(LARD_ERR_INVALID_ARGUMENT, "%s has a negative size", name);
-  if (t->dtype != LARD_DTYPE_F16 && t->dtype != LARD_DTYPE_BF16)
-    return fail(LARD_ERR_UNSUPPORTED, "%s dtype supports only fp16/bf16", name);
+  if (t->dtype != LARD_DTYPE_F16 && t->dtype != LARD_DTYPE_BF16 && t->dtype != LARD_DTYPE_F32)
+    return fail(LARD_ERR_UNSUPPORTED, "%s dtype supports only fp16/bf16/fp32", name);
   if (t->stride[3] != 1) return fail(LARD_ERR_INVALID_ARGUMENT, "%s last-dim stride must be 1", name);
+  const int64_t vec = t->dtype == LARD_DTYPE_F32 ? 4 : 8;  // elements per 16-byte load
   for (int i = 0; i < 3; ++i)
-    if (t->stride[i] % 8 != 0)
-      return fail(LARD_ERR_UNSUPPORTED, "%s strides must be multiples of 8 elements", name);
+    if (t->stride[i] % vec != 0)
+      return fail(LARD_ERR_UNSUPPORTED, "%s strides must be multiples of %d elements", name, (int)vec);
   if (reinterpret_cast<uintptr_t>(t->data) % 16 != 0)
     return fail(LARD_ERR_UNSUPPORTED, "%s data pointer must be 16-byte aligned", name);
   if (t->size[2] > (int64_t)1 << 30) return fail(LARD_ERR_UNSUPPORTED, "%s sequence length too large", name);
@@ -109,6 +111,7 @@ void fill_side(lard::SideArgs& s, const lard_tensor4* q, const lard_tensor4* k, 
   s.group = (int)(Hq / k->size[1]);
   s.dim = (int)q->size[3];
   s.bf16 = q->dtype == LARD_DTYPE_BF16;
+  s.f32 = q->dtype == LARD_DTYPE_F32;
   s.scale = scale;
   s.scale2 = scale * lard::kLog2e;
 }
@@ -147,6 +150,8 @@ int check_two_sided(const lard_tensor4* qs, const lard_tensor4* ks, const float*
   if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
   if (qs->size[0] != qt->size[0] || qs->size[1] != qt->size[1] || qs->size[2] != qt->size[2])
     return fail(LARD_ERR_INVALID_ARGUMENT, "student/teacher B/Hq/T must align");
+  if ((qs->dtype == LARD_DTYPE_F32) != (qt->dtype == LARD_DTYPE_F32))
+    return fail(LARD_ERR_UNSUPPORTED, "float32 inputs need float32 on both sides");
   const int64_t n = qs->size[0] * qs->size[1] * qs->size[2];
   if (n > 0 && (lse_s == nullptr || lse_t == nullptr)) return fail(LARD_ERR_INVALID_ARGUMENT, "lse must not be NULL");
   if ((rc = check_mask(mask, qs->size[0], qs->size[2])) != LARD_OK) return rc;
@@ -354,6 +359,8 @@ int check_batch(const lard_relation* rels, int nrel, const lard_mask* mask, floa
       return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: every relation must share B and T", r);
     if (xs.dtype != x0.dtype || xt.dtype != x0.dtype || xs.size[3] != x0.size[3] || xt.size[3] != x0.size[3])
       return fail(LARD_ERR_UNSUPPORTED, "relation %d: batched relations must share the dtype and head dim", r);
+    if (xs.dtype == LARD_DTYPE_F32)
+      return fail(LARD_ERR_UNSUPPORTED, "relation %d: float32 relations run one by one (stage kernels)", r);
     if (!lard::hot_supported((int)xs.size[3], (int)xt.size[3], true) || !hot_offsets_ok({&xs, &xt}, xs.size[2]))
       return fail(LARD_ERR_UNSUPPORTED, "relation %d: shape outside the batched kernels (D <= 128)", r);
     if (xs.size[1] <= 0) return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d has no heads", r);
@@ -582,6 +589,8 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
   if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
   if (qs->size[0] != qt->size[0] || qs->size[1] != qt->size[1] || qs->size[2] != qt->size[2])
     return fail(LARD_ERR_INVALID_ARGUMENT, "student/teacher B/Hq/T must align");
+  if ((qs->dtype == LARD_DTYPE_F32) != (qt->dtype == LARD_DTYPE_F32))
+    return fail(LARD_ERR_UNSUPPORTED, "float32 inputs need float32 on both sides");
   if ((rc = check_mask(mask, qs->size[0], qs->size[2])) != LARD_OK) return rc;
   if ((rc = check_scale(sm_scale_s, "sm_scale_s")) != LARD_OK) return rc;
   if ((rc = check_scale(sm_scale_t, "sm_scale_t")) != LARD_OK) return rc;
@@ -599,10 +608,11 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
     const int ds = (int)qs->size[3], dt = (int)qt->size[3];
     const bool same = qs->dtype == qt->dtype;
     const bool bf = qs->dtype == LARD_DTYPE_BF16;
+    const bool f32 = qs->dtype == LARD_DTYPE_F32;  // float32 runs the stage kernels
     const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
-    const bool hot = lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T) &&
+    const bool hot = !f32 && lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T) &&
                      hot_scales_ok(sm_scale_s, sm_scale_t);
-    if (hot || lard::fused_fwd_supported(ds, dt, same)) {
+    if (hot || (!f32 && lard::fused_fwd_supported(ds, dt, same))) {
       lard::HotArgs f{};
       fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
       fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
@@ -629,6 +639,18 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
                         "attn_kl_forward fused launch");
       }
       if (rc != LARD_OK) return rc;
+    } else if (f32) {
+      // float32: both LSEs and the KL in one double-precision pass
+      lard::FusedArgs g{};
+      fill_side(g.r.s, qs, ks, Hq, sm_scale_s);
+      fill_side(g.r.t, qt, kt, Hq, sm_scale_t);
+      fill_common(g.r, B, Hq, T, mask, causal);
+      g.lse_s_out = lse_s_out;
+      g.lse_t_out = lse_t_out;
+      g.row_out = w.loss.rows;
+      if ((rc = hip_status(timed(LARD_KERNEL_FORWARD, st, [&] { return lard::launch_fused_fwd_f32(g, st); }),
+                           "attn_kl_forward float32 launch")) != LARD_OK)
+        return rc;
     } else {
       // Stage A twice, then stage B (the reference's own composition).
       if ((rc = lard_lse_stats(qs, ks, mask, causal, sm_scale_s, lse_s_out, stream)) != LARD_OK) return rc;
@@ -658,7 +680,9 @@ size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64
   (void)self_relation;
   size_t bytes = 0;
   bwd_layout(nullptr, batch, heads, seq_len, &bytes);
-  return bytes;
+  // float32 inputs: both sides' LSEs in double (the refine pass)
+  const size_t f64 = align256((size_t)(2 * batch * heads * seq_len) * sizeof(double));
+  return bytes > f64 ? bytes : f64;
 }
 
 int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s, const lard_tensor4* qt,
@@ -688,8 +712,8 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
   a.lse_t_in = lse_t;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int ds = (int)qs->size[3], dt = (int)qt->size[3];
-  if (lard::hot_supported(ds, dt, qs->dtype == qt->dtype) && hot_offsets_ok({qs, ks, qt, kt}, T) &&
-      hot_scales_ok(sm_scale_s, sm_scale_t)) {
+  if (qs->dtype != LARD_DTYPE_F32 && lard::hot_supported(ds, dt, qs->dtype == qt->dtype) &&
+      hot_offsets_ok({qs, ks, qt, kt}, T) && hot_scales_ok(sm_scale_s, sm_scale_t)) {
     const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
@@ -721,6 +745,20 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                       "attn_kl_backward dk launch");
   }
   const int dps = padded_dim(ds), dpt = padded_dim(dt);
+  if (qs->dtype == LARD_DTYPE_F32) {
+    // float32: refine both LSEs in double first (the stored ones are float32
+    // roundings, too coarse for D = P_s - P_t of a near-identical pair)
+    const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    a.lse64_out = static_cast<double*>(workspace);
+    if ((rc = hip_status(lard::launch_refine_lse_f32(a, st), "attn_kl_backward float32 lse launch")) != LARD_OK)
+      return rc;
+    a.lse64_out = nullptr;
+    a.lse64_in = static_cast<const double*>(workspace);
+  }
   a.dq_out = dq_dst;
   a.dscale = self_relation ? nullptr : dloss;
   if ((rc = hip_status(timed(LARD_KERNEL_ROW_GRAD, st, [&] { return lard::launch_row_dq(a, dps, dpt, st); }),
@@ -861,6 +899,7 @@ int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* 
                    const int64_t* position_ids, int64_t pos_stride_b, void* out_t, void* out_s, void* stream) {
   int rc;
   if ((rc = check_tensor(x, "x")) != LARD_OK) return rc;
+  if (x->dtype == LARD_DTYPE_F32) return fail(LARD_ERR_UNSUPPORTED, "rope_pair supports only fp16/bf16");
   const int64_t B = x->size[0], H = x->size[1], T = x->size[2], D = x->size[3];
   if (D % 16 != 0) return fail(LARD_ERR_UNSUPPORTED, "rope_pair needs D to be a multiple of 16");
   if (B * H * T == 0) return ok();

@@ -40,7 +40,7 @@ enum RowMode : int {
 
 // One relation q.k^T of the problem (student or teacher).
 struct SideArgs {
-  const u16* q;       // [B, Hq, T, D] elements (bf16 or f16 bits)
+  const u16* q;       // [B, Hq, T, D] elements (bf16 or f16 bits; floats when f32)
   const u16* k;       // [B, Hkv, T, D]
   int64_t q_sb, q_sh, q_st;  // element strides (D stride is 1)
   int64_t k_sb, k_sh, k_st;
@@ -48,6 +48,7 @@ struct SideArgs {
   int group;          // Hq / Hkv  (kv head = h / group, kernel_A.py:77)
   int dim;            // D (<= the kernel's padded D)
   int bf16;           // 1: bfloat16, 0: float16
+  int f32;            // 1: float32 (q / k point to floats; stage_f32.hip kernels)
   float scale;        // softmax scale (natural)
   float scale2;       // scale * log2(e)
 };
@@ -74,6 +75,11 @@ struct RelArgs {
   // a batched loss (multiplies the per-row KL, and the gradient wherever
   // dscale is applied).
   const float* weight;
+  // float32-input kernels only: the double-precision LSEs of both sides,
+  // [2][B, Hq, T] (student, then teacher).  The refine pass writes them; the
+  // dq / dk passes read them (instead of lse_*_in) when non-null.
+  double* lse64_out;
+  const double* lse64_in;
 };
 
 // Outputs of the fused forward (one pass: both LSEs and the per-row KL).

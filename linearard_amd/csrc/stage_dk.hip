@@ -2,6 +2,7 @@
 // key tile, no atomics (replaces the atomic_add of kernel_C.py:242-253).
 #include "stage_kernels.h"
 #include "stage_dispatch.h"
+#include "stage_f32.h"
 
 namespace lard {
 
@@ -18,6 +19,7 @@ static hipError_t launch_dk(const RelArgs& a, int dpt, dim3 grid, hipStream_t st
 }
 
 hipError_t launch_col_dk(const RelArgs& a, int dps, int dpt, hipStream_t stream) {
+  if (a.s.f32) return launch_col_dk_f32(a, stream);  // float32 inputs (both sides)
   const dim3 grid((a.T + kStageRows - 1) / kStageRows, a.B * a.s.hkv);
   switch (dps) {
 #define X(DP, unused) \

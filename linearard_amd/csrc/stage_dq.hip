@@ -1,6 +1,7 @@
 // Stage C row-side launcher: dq (kernel_C.py:388-447).
 #include "stage_kernels.h"
 #include "stage_dispatch.h"
+#include "stage_f32.h"
 
 namespace lard {
 
@@ -17,6 +18,7 @@ static hipError_t launch_dq(const RelArgs& a, int dpt, dim3 grid, hipStream_t st
 }
 
 hipError_t launch_row_dq(const RelArgs& a, int dps, int dpt, hipStream_t stream) {
+  if (a.s.f32) return launch_row_dq_f32(a, stream);  // float32 inputs (both sides)
   const dim3 grid((a.T + kStageRows - 1) / kStageRows, a.B * a.Hq);
   switch (dps) {
 #define X(DP, unused) \

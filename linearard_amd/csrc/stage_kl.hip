@@ -1,6 +1,7 @@
 // Stage B launcher: per-row KL given both LSE vectors (kernel_B.py:340-389).
 #include "stage_kernels.h"
 #include "stage_dispatch.h"
+#include "stage_f32.h"
 
 namespace lard {
 
@@ -17,6 +18,7 @@ static hipError_t launch_kl(const RelArgs& a, int dpt, dim3 grid, hipStream_t st
 }
 
 hipError_t launch_row_kl(const RelArgs& a, int dps, int dpt, hipStream_t stream) {
+  if (a.s.f32) return launch_row_kl_f32(a, stream);  // float32 inputs (both sides)
   const dim3 grid((a.T + kStageRows - 1) / kStageRows, a.B * a.Hq);
   switch (dps) {
 #define X(DP, unused) \

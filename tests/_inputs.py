@@ -12,7 +12,7 @@ import torch
 
 from oracle import attn_kl as O
 
-TORCH_DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16}
+TORCH_DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
 
 
 def rounded(x, dtype):

@@ -39,7 +39,7 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     t.stride[:] = [256, 128, 16, 1]
     t.dtype = 7
     rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
-    assert rc == -2 and b"fp16/bf16" in L.lard_last_error()
+    assert rc == -2 and b"fp16/bf16/fp32" in L.lard_last_error()
     t.dtype = 0
     t.stride[3] = 2
     rc = L.lard_lse_stats(ctypes.byref(t), ctypes.byref(t), ctypes.byref(m), 1, 0.1, 64, None)
@@ -61,12 +61,14 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert L.lard_kl_forward_workspace_bytes(0, 3, 5) == 0
     # forward of the autograd path adds one validity byte per (padded) token
     assert L.lard_attn_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8 + 4 * 4096
-    # backward: validity bytes and 2 normalisers per (padded) row
+    # backward: validity bytes and 2 normalisers per (padded) row, or, when
+    # larger, the float32 path's two double LSEs per row
     B, H, T, D = 2, 8, 1000, 64
     Tp = 1024
     tail = B * Tp + 2 * B * H * Tp * 4
-    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 1) == tail
-    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 0) == tail
+    f64 = (2 * B * H * T * 8 + 255) // 256 * 256
+    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 1) == max(tail, f64)
+    assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 0) == max(tail, f64)
     assert L.lard_attn_kl_backward_workspace_bytes(0, H, H, T, D, 0) == 0
 
 

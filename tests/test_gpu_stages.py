@@ -156,8 +156,8 @@ def test_stage_b_is_deterministic(gpu_available):
 def test_wrapper_validation_messages(gpu_available):
     from linearard_amd.attention_KL import kl_forward, lse_stats
 
-    q = torch.zeros((1, 2, 8, 16), dtype=torch.float32, device="cuda")
-    with pytest.raises(AssertionError, match="q dtype supports only fp16/bf16"):
+    q = torch.zeros((1, 2, 8, 16), dtype=torch.float64, device="cuda")
+    with pytest.raises(AssertionError, match="q dtype supports only fp16/bf16/fp32"):
         lse_stats(q, q)
     h = torch.zeros((1, 3, 8, 16), dtype=torch.bfloat16, device="cuda")
     k = torch.zeros((1, 2, 8, 16), dtype=torch.bfloat16, device="cuda")
