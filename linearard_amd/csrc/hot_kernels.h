@@ -350,14 +350,20 @@ __device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int
 #pragma unroll
     for (int e = 0; e < EP; e += 2) {
       const int r = kk * EP + e;
-      const float pt0 = fast_exp2(fmaf(st[r], c2t, R.nm_t));
-      const float pt1 = fast_exp2(fmaf(st[r + 1], c2t, R.nm_t));
-      s0 += fast_exp2(fmaf(ss[r], c2s, R.nm_s));
-      s1 += fast_exp2(fmaf(ss[r + 1], c2s, R.nm_s));
+      // all exponent arguments first, then the four exponentials back to
+      // back, then the sums: no fma -> exp -> add dependency at issue
+      float xt0 = fmaf(st[r], c2t, R.nm_t), xt1 = fmaf(st[r + 1], c2t, R.nm_t);
+      float xs0 = fmaf(ss[r], c2s, R.nm_s), xs1 = fmaf(ss[r + 1], c2s, R.nm_s);
+      const float d0 = fmaf(st[r], ratio, -ss[r]), d1 = fmaf(st[r + 1], ratio, -ss[r + 1]);
+      asm volatile("" : "+v"(xt0), "+v"(xt1), "+v"(xs0), "+v"(xs1));
+      const float pt0 = fast_exp2(xt0), pt1 = fast_exp2(xt1);
+      const float ps0 = fast_exp2(xs0), ps1 = fast_exp2(xs1);
+      s0 += ps0;
+      s1 += ps1;
       t0 += pt0;
       t1 += pt1;
-      a0 = fmaf(pt0, fmaf(st[r], ratio, -ss[r]), a0);
-      a1 = fmaf(pt1, fmaf(st[r + 1], ratio, -ss[r + 1]), a1);
+      a0 = fmaf(pt0, d0, a0);
+      a1 = fmaf(pt1, d1, a1);
     }
     // the empty asm consumes this k-step's sums, so no IR pass can sink their
     // arithmetic past the scheduling barrier
