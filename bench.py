@@ -106,6 +106,44 @@ def rope_pair_ntk(B, H, n, d, base, base_scale, seed=0, outliers=4):
     return rotate(base * base_scale), rotate(base)  # student, teacher
 
 
+def host_cpu():
+    """The host CPU's model name (from /proc/cpuinfo where there is one)."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def gpu_clock(torch):
+    """What the box runs: the device's maximum shader clock (MHz) from its
+    properties and, where the driver exposes it, the active sclk level."""
+    out = {}
+    try:
+        props = torch.cuda.get_device_properties(0)
+        rate = getattr(props, "clock_rate", None)
+        if rate:
+            out["max_sclk_mhz"] = rate / 1000.0
+        out["device"] = props.name
+    except Exception:  # properties are informational only
+        pass
+    import glob
+
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            with open(path) as fh:
+                active = [ln.strip() for ln in fh if ln.strip().endswith("*")]
+        except OSError:
+            continue
+        if active:
+            out["active_sclk"] = active[0]
+            break
+    return out
+
+
 def algorithmic_flops(B, H, n, d):
     pairs = n * (n + 1) // 2
     return 12 * d * pairs * B * H
@@ -130,7 +168,7 @@ def cpu_baseline(n, d, relations):
         "cores": int(threads),
         "kind": "port",
         "sample": f"1 of {relations} (b,h) relations at n={n}, d={d}, causal, fwd+bwd, float32 numpy "
-                  f"(oracle.attn_kl.self_relation_chunked), {dt:.1f} s; host {platform.processor() or platform.machine()}",
+                  f"(oracle.attn_kl.self_relation_chunked), {dt:.1f} s; host {host_cpu()}",
         "tflops": 12 * d * (n * (n + 1) // 2) / dt / 1e12,
     }
 
@@ -378,7 +416,7 @@ def run_logits(args):
             "value": rows / dt, "unit": "positions/s", "cores": 1, "kind": "port",
             "sample": f"{rows} kept positions of V={V}, forward + both gradients, float64 numpy "
                       f"(oracle.logits_kl), {reps} repetitions in {reps * dt:.1f} s; host "
-                      f"{platform.processor() or platform.machine()}",
+                      f"{host_cpu()}",
         }
     print(json.dumps(out))
 
@@ -593,6 +631,7 @@ def main():
             kernel_ms[name] = total.value / count.value
     peak = torch.cuda.max_memory_allocated(dev) - base_mem
 
+    step_ms = sorted(f[0].elapsed_time(b[1]) for f, b in zip(ev["fwd"], ev["bwd"]))
     fwd_ms = sum(a.elapsed_time(b) for a, b in ev["fwd"]) / len(ev["fwd"])
     bwd_ms = sum(a.elapsed_time(b) for a, b in ev["bwd"]) / len(ev["bwd"])
     ms = elapsed / args.steps * 1e3
@@ -625,7 +664,9 @@ def main():
                    "B": B, "H": H, "n": n, "d": d, "causal": True},
         "tflops": flops / (ms * 1e-3) / 1e12,
         "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS,
+        "median_step_ms": step_ms[len(step_ms) // 2],
         "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
+        "gpu_clock": gpu_clock(torch),
         "kernel_ms": kernel_ms,
         "peak_hbm_bytes": int(peak),
         "loss": float(loss.item()),
