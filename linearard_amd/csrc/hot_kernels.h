@@ -837,6 +837,34 @@ __device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
   }
 }
 
+
+// GEMM1 of one sub-block (S = A B^T for both relations; A: this lane's row
+// r0 + l32 of the swizzled student tile, the teacher tile following it; B:
+// the register operands fb_s, fb_t), operands read PD MFMAs ahead.
+template <int DP, bool BF, int PD = 4>
+__device__ __forceinline__ void gemm1(const u16* tile, int r0, int l32, int half, const u16x8* fb_s,
+                                      const u16x8* fb_t, f32x16& ss, f32x16& st) {
+  constexpr int N = 2 * (DP / 16);  // student / teacher alternating
+  u16x8 op[N];
+  auto load = [&](int i) {
+    op[i] = *reinterpret_cast<const u16x8*>(row_chunk<DP>(tile, r0 + l32, 2 * (i >> 1) + half) +
+                                            ((i & 1) ? kTile * DP : 0));
+  };
+#pragma unroll
+  for (int i = 0; i < PD && i < N; ++i) load(i);
+  ss = (f32x16)(0.f);
+  st = (f32x16)(0.f);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + PD < N) load(i + PD);
+    if (i & 1)
+      st = mfma32<BF>(op[i], fb_t[i >> 1], st);
+    else
+      ss = mfma32<BF>(op[i], fb_s[i >> 1], ss);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ----------------------------------------------------------------------------
 // backward, column side: dk = sm_scale_s sum_{h in group} D^T Q_s
 // ----------------------------------------------------------------------------
@@ -932,7 +960,7 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
         if (causal && gsb < diag_sb) continue;
         f32x16 ss, st;
         __builtin_amdgcn_s_setprio(1);  // the MFMA-feeding wave goes first (see mfma_phase)
-        sub_scores<DP, BF>(lq[buf][0], 32 * sb, l32, half, fk_s, fk_t, ss, st);
+        gemm1<DP, BF, 4>(lq[buf][0], 32 * sb, l32, half, fk_s, fk_t, ss, st);
         __builtin_amdgcn_s_setprio(0);
         float dd[16];
 #pragma unroll
@@ -952,13 +980,17 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
             dd[r] = off + lim >= 0 ? dd[r] : 0.f;
           }
         }
+        constexpr int N2 = 2 * NDB, P2 = N2 < 4 ? N2 : 4;
+        u16x8 op2[N2];
+#pragma unroll
+        for (int i = 0; i < P2; ++i) op2[i] = tro.read(lq[buf][0], sb, i / NDB, i % NDB);
+        const u16x8 bop[2] = {pack_d<BF>(dd), pack_d<BF>(dd + 8)};  // D cast to the input dtype (kernel_C.py:233)
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const u16x8 bop = pack_d<BF>(dd + 8 * m);  // D cast to the input dtype (kernel_C.py:233)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            dk[db] = mfma32<BF>(tro.read(lq[buf][0], sb, m, db), bop, dk[db]);
+        for (int i = 0; i < N2; ++i) {
+          if (i + P2 < N2) op2[i + P2] = tro.read(lq[buf][0], sb, (i + P2) / NDB, (i + P2) % NDB);
+          dk[i % NDB] = mfma32<BF>(op2[i], bop[i / NDB], dk[i % NDB]);
+          __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_setprio(0);
       }
