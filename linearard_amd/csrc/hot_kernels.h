@@ -325,11 +325,16 @@ __device__ __forceinline__ void sub_scores(const u16* ks, int r0, int l32, int h
 // of 16/KS of the current sub-block's elements, and scheduling barriers keep
 // that order, so the matrix unit and the VALU work at the same time within
 // the wave.  LDS operands are read PD k-steps ahead.
-template <int DP, bool BF, int PD = 2>
+//
+// PRE_IN: the first k-step's operands were read by the previous step into
+// pre (the K/Q chunks of this sub-block); PRE_OUT: the last k-step also reads
+// the first k-step's operands of row `pre_row` of the same tile into pre,
+// for the next step.
+template <int DP, bool BF, int PD = 2, bool PRE_IN = false, bool PRE_OUT = false>
 __device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int half,
                                                      const u16x8* fq_s, const u16x8* fq_t, f32x16& ns, f32x16& nt,
                                                      const f32x16& ss, const f32x16& st, const SoftRow& R, float c2s,
-                                                     float c2t, float ratio) {
+                                                     float c2t, float ratio, u16x8* pre = nullptr, int pre_row = 0) {
   constexpr int KS = DP / 16, EP = 16 / KS;
   u16x8 os[KS], ot[KS];
   auto load = [&](int kk) {
@@ -338,13 +343,25 @@ __device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int
     ot[kk] = *reinterpret_cast<const u16x8*>(p + kTile * DP);  // same slot of the teacher tile
   };
 #pragma unroll
-  for (int kk = 0; kk < PD && kk < KS; ++kk) load(kk);
+  for (int kk = 0; kk < PD && kk < KS; ++kk) {
+    if (PRE_IN && kk == 0) {
+      os[0] = pre[0];
+      ot[0] = pre[1];
+    } else {
+      load(kk);
+    }
+  }
   ns = (f32x16)(0.f);
   nt = (f32x16)(0.f);
   float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     if (kk + PD < KS) load(kk + PD);
+    if (PRE_OUT && kk == KS - 1) {
+      const u16* p = row_chunk<DP>(ks, pre_row, half);
+      pre[0] = *reinterpret_cast<const u16x8*>(p);
+      pre[1] = *reinterpret_cast<const u16x8*>(p + kTile * DP);
+    }
     ns = mfma32<BF>(os[kk], fq_s[kk], ns);
     nt = mfma32<BF>(ot[kk], fq_t[kk], nt);
 #pragma unroll
@@ -465,13 +482,21 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
       mask_block(x.s, x.t, (unsigned)(x.tm >> (32 * sb + 4 * half)), my_i - first, causal);
     }
   };
-  // softmax of cur (tile it, half sb) while the scores of nxt (tile it2, half sb2) run
+  // softmax of cur (tile it, half sb) while the scores of nxt (tile it2, half sb2) run.
+  // Scoring half 0 of a tile also reads the first operands of its half 1
+  // (same tile, no barrier between), which the next step scores.
+  u16x8 pre[2];
   auto step = [&](Sub& cur, int it, int sb, Sub& nxt, int it2, int sb2) {
     prepare(cur, it, sb);
     const int buf = it2 % kBufs;
     nxt.tm = __ballot(ltok[buf][w][lane] != 0);  // read now: the buffer is refilled before its softmax
-    const BlockSums bs = scores_and_sums<DP, BF>(lk[buf][0], 32 * sb2 + l32, half, fq_s, fq_t, nxt.s,
-                                                 nxt.t, cur.s, cur.t, R, c2s, c2t, ratio);
+    BlockSums bs;
+    if (sb2 == 0)
+      bs = scores_and_sums<DP, BF, 2, false, true>(lk[buf][0], l32, half, fq_s, fq_t, nxt.s, nxt.t, cur.s, cur.t, R,
+                                                   c2s, c2t, ratio, pre, 32 + l32);
+    else
+      bs = scores_and_sums<DP, BF, 2, true, false>(lk[buf][0], 32 + l32, half, fq_s, fq_t, nxt.s, nxt.t, cur.s,
+                                                   cur.t, R, c2s, c2t, ratio, pre);
     add_block(cur.s, cur.t, bs, R, c2s, c2t, ratio);
   };
   auto last = [&](Sub& cur, int it, int sb) {
@@ -496,6 +521,11 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   const int nsub = 2 * ntiles;
   Sub A, B;
   scores(A, 0, 0);
+  {  // the first operands of half 1 of tile 0 (see step)
+    const u16* p = row_chunk<DP>(lk[0][0], 32 + l32, half);
+    pre[0] = *reinterpret_cast<const u16x8*>(p);
+    pre[1] = *reinterpret_cast<const u16x8*>(p + kTile * DP);
+  }
   for (int k = 0;; k += 2) {
     step(A, k >> 1, 0, B, k >> 1, 1);
     if (k + 2 >= nsub) {
