@@ -1,4 +1,5 @@
-"""attn_kl_align forward + backward captured in a HIP graph and replayed.
+"""Forward + backward captured in a HIP graph and replayed: attn_kl_align,
+the batched relation loss (relation_kl_loss) and the logits KL.
 
 The library only launches kernels on the caller's stream: no allocation, no
 memset node, no host synchronisation (the drop-in boundary's graph-capture
@@ -68,3 +69,82 @@ def test_fwd_bwd_graph_replays_match_eager(gpu_available, masked):
         assert torch.equal(got_loss, want_loss), (rep, got_loss.item(), want_loss.item())
         assert torch.equal(got_grad, want_grad), rep
         assert got_loss.item() > 0.0
+
+
+def _capture_and_check(run, inputs, redraw, reps=3):
+    """Warm up, capture run(*inputs) -> (loss, *grads) once, then for each
+    replay: redraw the inputs in place, replay, and compare with run() on
+    fresh copies of the same values."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run(*inputs)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run(*inputs)
+    for rep in range(reps):
+        values = redraw(rep)
+        with torch.no_grad():
+            for dst, v in zip(inputs, values):
+                dst.copy_(v)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs]
+        fresh = [v.clone().requires_grad_(src.requires_grad) for src, v in zip(inputs, values)]
+        want = run(*fresh)
+        torch.cuda.synchronize()
+        for i, (x, y) in enumerate(zip(got, want)):
+            assert torch.equal(x, y), (rep, i)
+
+
+def test_batched_relation_loss_graph_replays_match_eager(gpu_available):
+    """relation_kl_loss (train.py:369-410 in batched launches): descriptors in
+    the kernel arguments, per-relation weights as device scalars."""
+    from linearard_amd.attention_KL import relation_kl_loss
+
+    B, T, D, layers = 1, 512, 128, 2
+    a = 1 / math.sqrt(D)
+    g = torch.Generator(device="cuda").manual_seed(23)
+    heads = [h for _ in range(layers) for h in (8, 2, 2)]
+
+    def redraw(rep):
+        pairs = [_draw(g, (B, h, T, D), 0.2 + 0.05 * rep) for h in heads]
+        return [p[0] for p in pairs] + [p[1] for p in pairs]
+
+    first = redraw(0)
+    n = len(heads)
+    inputs = [v.clone().requires_grad_(i < n) for i, v in enumerate(first)]
+
+    def run(*xs):
+        s, t = xs[:n], xs[n:]
+        loss = relation_kl_loss(s[0::3], s[1::3], s[2::3], t[0::3], t[1::3], t[2::3], sm_scale_s=a, sm_scale_t=a)
+        grads = torch.autograd.grad(loss, list(s))
+        return (loss, *grads)
+
+    _capture_and_check(run, inputs, redraw)
+
+
+def test_logits_kl_graph_replays_match_eager(gpu_available):
+    """logits_kl (train.py:412-420): forward, finish and gradient kernels."""
+    from linearard_amd.logits_kl import logits_kl
+
+    B, K, V = 2, 64, 32000
+    g = torch.Generator(device="cuda").manual_seed(29)
+
+    def redraw(rep):
+        t = torch.randn((B, K, V), device="cuda", generator=g)
+        s = t + (0.5 + 0.1 * rep) * torch.randn((B, K, V), device="cuda", generator=g)
+        return [s.to(torch.bfloat16), t.to(torch.bfloat16)]
+
+    first = redraw(0)
+    inputs = [first[0].clone().requires_grad_(True), first[1].clone()]
+
+    def run(s, t):
+        loss = logits_kl(t, s, temperature=2.0)
+        (gs,) = torch.autograd.grad(loss, s)
+        return loss, gs
+
+    _capture_and_check(run, inputs, redraw)
