@@ -1,4 +1,5 @@
-"""Parity at the BASELINE configurations' full sizes (cfg2, cfg3, cfg4 shapes).
+"""Parity at the BASELINE configurations' full sizes (cfg2, cfg3, cfg4 shapes)
+and at n = 131072.
 
 At these sizes the oracle cannot check every head within seconds.  So each
 test checks one full-length head against the chunked CPU oracle
@@ -151,3 +152,55 @@ def test_cfg3_batched_relation_loss_equals_the_loop(gpu_available):
         for x1, x2 in zip(l1, l2):
             g1, g2 = x1.grad.float(), x2.grad.float()
             assert (g1 - g2).abs().max() <= 1e-2 * g2.abs().max() + 1e-6
+
+
+def test_long_context_128k_and_the_strided_view(gpu_available):
+    """n = 131072 (4x cfg4), one head.  It checks:
+    - loss and gradient are finite, and the loss is positive;
+    - the student LSE of the first 2048 rows equals the chunked oracle's, and
+      the last row's equals scipy's logsumexp;
+    - the same head read by the batched API through the permuted view of a
+      [B, T, H, D] tensor (row stride H*d) gives the same loss and gradient;
+    - identical relations give exactly 0."""
+    from scipy.special import logsumexp
+
+    from linearard_amd.attention_KL import attn_kl_align, attn_kl_align_batched, lse_stats
+
+    B, H, n, d = 1, 4, 131072, 128
+    a = 1 / math.sqrt(d)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    raw_t = torch.randn((B, n, H, d), device="cuda", generator=g)
+    raw_s = raw_t + 0.1 * torch.randn((B, n, H, d), device="cuda", generator=g)
+    bt, bs = raw_t.to(torch.bfloat16), raw_s.to(torch.bfloat16)
+    del raw_t, raw_s
+    xt = bt.permute(0, 2, 1, 3)[:, 1:2].contiguous()  # head 1: [1, 1, n, d]
+    xs = bs.permute(0, 2, 1, 3)[:, 1:2].contiguous().requires_grad_(True)
+    loss = attn_kl_align(xs, xs, xt, xt, causal=True, sm_scale_s=a, sm_scale_t=a)
+    loss.backward()
+    assert math.isfinite(loss.item()) and loss.item() > 0.0
+    assert bool(torch.isfinite(xs.grad).all())
+
+    base = bs.detach().clone().requires_grad_(True)  # the hook's [B, T, H, D] layout, read in place
+    w = torch.ones(1, device="cuda", dtype=torch.float32)
+    lb = attn_kl_align_batched([base.permute(0, 2, 1, 3)[:, 1:2]], [bt.permute(0, 2, 1, 3)[:, 1:2]], w,
+                               causal=True, sm_scale_s=a, sm_scale_t=a)
+    lb.backward()
+    assert abs(lb.item() - loss.item()) <= 1e-6 * loss.item(), (lb.item(), loss.item())
+    gb = base.grad.permute(0, 2, 1, 3)[:, 1:2].float()
+    assert (gb - xs.grad.float()).abs().max() <= 1e-2 * xs.grad.float().abs().max()
+    assert not bool(base.grad[:, :, 0].any())  # the other heads get no gradient
+
+    lse = lse_stats(xs.detach(), xs.detach(), causal=True, sm_scale=a)[0, 0].double().cpu().numpy()
+    x_s = xs.detach()[0, 0].float().cpu().numpy()
+    x_t = xt[0, 0].float().cpu().numpy()
+    _, _, ref_lse, _, ref_kl = O.self_relation_chunked(x_s, x_t, True, a, a, chunk=512, dtype=np.float64,
+                                                       want_grad=False, rows_subset=2048)
+    assert np.abs(lse[:2048] - ref_lse[:2048]).max() <= 1e-4
+    assert ref_kl[:2048].min() >= -1e-9
+    last = logsumexp(a * (x_s.astype(np.float64) @ x_s[-1].astype(np.float64)))
+    assert abs(lse[-1] - last) <= 1e-4 * max(1.0, abs(last)), (lse[-1], last)
+
+    same = xt.clone().requires_grad_(True)
+    z = attn_kl_align(same, same, xt, xt, causal=True, sm_scale_s=a, sm_scale_t=a)
+    z.backward()
+    assert z.item() == 0.0 and not bool(same.grad.any())
