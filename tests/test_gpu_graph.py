@@ -1,5 +1,6 @@
 """Forward + backward captured in a HIP graph and replayed: attn_kl_align,
-the batched relation loss (relation_kl_loss) and the logits KL.
+the batched relation loss (relation_kl_loss), the logits KL, and the RoPE
+pair producer feeding distillation_loss.
 
 The library only launches kernels on the caller's stream: no allocation, no
 memset node, no host synchronisation (the drop-in boundary's graph-capture
@@ -146,5 +147,45 @@ def test_logits_kl_graph_replays_match_eager(gpu_available):
         loss = logits_kl(t, s, temperature=2.0)
         (gs,) = torch.autograd.grad(loss, s)
         return loss, gs
+
+    _capture_and_check(run, inputs, redraw)
+
+
+def test_rope_pair_and_distillation_loss_graph_replays_match_eager(gpu_available):
+    """The RoPE pair producer feeding distillation_loss (train.py:360-423,
+    lam_L != 0, masked), forward + backward, in one graph."""
+    from linearard_amd.distill import distillation_loss
+    from linearard_amd.rope import rope_pair
+
+    B, T, D, H, Hkv, L, K, V = 2, 256, 128, 4, 2, 2, 16, 1024
+    g = torch.Generator(device="cuda").manual_seed(31)
+    mask = torch.ones((B, T), device="cuda", dtype=torch.int64)
+    mask[1, T - 40:] = 0
+    shapes = [(B, T, h, D) for _ in range(L) for h in (H, Hkv, Hkv)]  # per layer: q, k, v as the hook sees them
+
+    def redraw(rep):
+        pre = [torch.randn(sh, device="cuda", generator=g).to(torch.bfloat16) for sh in shapes]
+        t_log = torch.randn((B, K, V), device="cuda", generator=g)
+        s_log = t_log + (0.3 + 0.1 * rep) * torch.randn((B, K, V), device="cuda", generator=g)
+        return pre + [s_log.to(torch.bfloat16), t_log.to(torch.bfloat16)]
+
+    first = redraw(0)
+    n = len(shapes)
+    inputs = [v.clone().requires_grad_(i == n) for i, v in enumerate(first)]  # the student logits take a gradient
+
+    def run(*xs):
+        pre, s_log, t_log = xs[:n], xs[n], xs[n + 1]
+        qs, qt, ks, kt, vs, vt = [], [], [], [], [], []
+        for li in range(L):
+            q, k, v = (pre[3 * li + j].permute(0, 2, 1, 3) for j in range(3))
+            q_s, q_t = rope_pair(q, 10000.0, {"rope_type": "linear", "factor": 4.0})
+            k_s, k_t = rope_pair(k, 10000.0, {"rope_type": "linear", "factor": 4.0})
+            qs.append(q_s.detach().requires_grad_(True)); qt.append(q_t)
+            ks.append(k_s.detach().requires_grad_(True)); kt.append(k_t)
+            vs.append((v + 0.01).detach().requires_grad_(True)); vt.append(v)
+        out = distillation_loss(qs, ks, vs, qt, kt, vt, t_logits=t_log, s_logits=s_log, attn_mask=mask,
+                                lam_A=1.0, lam_L=0.5, temperature=2.0)
+        grads = torch.autograd.grad(out.loss, qs + ks + vs + [s_log])
+        return (out.loss, out.attn_loss, out.logits_loss, *grads)
 
     _capture_and_check(run, inputs, redraw)
