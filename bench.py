@@ -82,7 +82,7 @@ def rope_pair(B, H, n, d, pos_scale, base, seed=0, outliers=4):
 
 
 def rope_pair_ntk(B, H, n, d, base, base_scale, seed=0, outliers=4):
-    """Teacher/student pair for SURVEY cfg3: the same pre-RoPE vectors with
+    """Teacher/student pair for the benchmark's cfg3: the same pre-RoPE vectors with
     per-head std ~ U(0.5, 2), rotated at positions p with RoPE base `base`
     (teacher) and `base * base_scale` (student), HF rotate_half layout."""
     import torch
@@ -188,7 +188,7 @@ def traffic_summary(config):
 
 def run_layers(args):
     """The train.py relation loss (Q/Q + K/K + V/V per layer, train.py:369-410)
-    over `--layers` layers at SURVEY cfg3's shapes (B=1, n=8192, d=128, Q/Q
+    over `--layers` layers at the benchmark's cfg3 shapes (B=1, n=8192, d=128, Q/Q
     32 heads, K/K and V/V 8 heads; teacher RoPE base 5e5, student base x8),
     fwd+bwd, two ways: the batched launches (relation_kl_loss) and the
     reference caller's loop of attn_kl_align calls."""
@@ -422,7 +422,7 @@ def run_logits(args):
 
 
 def run_step(args):
-    """The loss side of one distillation step at SURVEY cfg5 (train.py:323-424
+    """The loss side of one distillation step at the benchmark's cfg5 (train.py:323-424
     for a Mistral-7B-v0.1-shaped model): 32 layers x (Q/Q 32 heads, K/K 8,
     V/V 8), B=2, n=16384, d=128, causal, all-ones PG19 mask; teacher RoPE
     base 1e4 at positions p, student linear interpolation x4; kept-position
@@ -538,8 +538,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; the multi-GPU sharding is a design note "
-                                   "(DESIGN.md), not a launched path", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU; sharding over several GPUs is designed "
+                                   "(split over (b, h) relations), not launched", "n_gpus": args.gpus}))
         sys.exit(2)
     if args.workload == "layers":
         run_layers(args)
