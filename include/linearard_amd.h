@@ -216,12 +216,15 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
  * contiguous [B, H, T, D] of x's dtype:
  *   out[i]       = R(R(x[i] c_i) + R(-x[i+D/2] s_i)),
  *   out[i + D/2] = R(R(x[i+D/2] c_i) + R(x[i] s_i)),
- * c_i, s_i = R(cos / sin of pos * inv_freq[i]) (the angle one float32
- * product), R the rounding to x's dtype after every operation.
- * inv_freq_t / inv_freq_s: device float32 [D/2]; position_ids: device int64
+ * c_i, s_i = R(cos / sin of pos * inv_freq[i], times att) (the angle one
+ * float32 product, then the float32 product with att), R the rounding to x's
+ * dtype after every operation.  inv_freq_t / inv_freq_s: device float32
+ * [D/2], any HF rope type's frequencies (default, linear, dynamic NTK, yarn,
+ * longrope, llama3, or another base); att_t / att_s: that type's
+ * attention_scaling (1 unless yarn / longrope); position_ids: device int64
  * [B, T] with batch stride pos_stride_b, or NULL for 0..T-1.
  */
-int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s,
+int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s, float att_t, float att_s,
                    const int64_t* position_ids, int64_t pos_stride_b, void* out_t, void* out_s, void* stream);
 
 /*

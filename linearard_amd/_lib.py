@@ -102,8 +102,8 @@ SIGNATURES = {
     "lard_attn_kl_batched_backward": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
                                                      ctypes.c_float, _FP, _FP, ctypes.c_void_p, ctypes.c_size_t,
                                                      ctypes.c_void_p]),
-    "lard_rope_pair": (ctypes.c_int, [_T4P, _FP, _FP, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-                                      ctypes.c_void_p, ctypes.c_void_p]),
+    "lard_rope_pair": (ctypes.c_int, [_T4P, _FP, _FP, ctypes.c_float, ctypes.c_float, ctypes.c_void_p,
+                                      ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "lard_logits_kl_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "lard_logits_kl_forward": (ctypes.c_int, [_LP, _LP, ctypes.c_float, _FP, _FP, _FP, _FP, ctypes.c_void_p,
                                               ctypes.c_size_t, ctypes.c_void_p]),

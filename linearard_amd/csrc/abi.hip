@@ -224,10 +224,12 @@ LossWs loss_layout(void* base, int64_t n, size_t* bytes) {
   return w;
 }
 
-// Forward of the autograd path: loss regions + token validity.
+// Forward of the autograd path: loss regions + token validity + the first
+// two valid tokens of each sequence.
 struct FwdWs {
   LossWs loss;
   unsigned char* tok_ok;
+  int* first2;
 };
 
 FwdWs fwd_layout(void* base, int64_t B, int64_t H, int64_t T, size_t* bytes) {
@@ -237,14 +239,17 @@ FwdWs fwd_layout(void* base, int64_t B, int64_t H, int64_t T, size_t* bytes) {
   Carver c(base != nullptr ? static_cast<char*>(base) + loss_bytes : nullptr);
   const int64_t Tp = padded_len(T);
   w.tok_ok = c.take<unsigned char>(B * Tp);
+  w.first2 = c.take<int>(2 * B);
   if (bytes != nullptr) *bytes = loss_bytes + c.bytes();
   return w;
 }
 
-// Backward of the autograd path: token validity and the log2-domain row
-// normalisers (the size depends on B, Hq and T only).
+// Backward of the autograd path: token validity, the first two valid tokens
+// of each sequence and the log2-domain row normalisers (the size depends on
+// B, Hq and T only).
 struct BwdWs {
   unsigned char* tok_ok;
+  int* first2;
   float* nl_s;
   float* nl_t;
 };
@@ -254,6 +259,7 @@ BwdWs bwd_layout(void* base, int64_t B, int64_t Hq, int64_t T, size_t* bytes) {
   BwdWs w;
   const int64_t Tp = padded_len(T);
   w.tok_ok = c.take<unsigned char>(B * Tp);
+  w.first2 = c.take<int>(2 * B);
   w.nl_s = c.take<float>(B * Hq * Tp);
   w.nl_t = c.take<float>(B * Hq * Tp);
   if (bytes != nullptr) *bytes = c.bytes();
@@ -319,6 +325,7 @@ hipError_t timed(int kernel, hipStream_t st, F&& launch) {
 struct BatchWs {
   LossWs loss;
   unsigned char* tok_ok;
+  int* first2;
   float* nl_s;
   float* nl_t;
 };
@@ -336,6 +343,7 @@ BatchWs batch_layout(void* base, const lard_relation* rels, int nrel, size_t* by
   w.loss = loss_layout(base, rows, &loss_bytes);
   Carver c(base != nullptr ? static_cast<char*>(base) + loss_bytes : nullptr);
   w.tok_ok = c.take<unsigned char>(rels[0].xs.size[0] * padded_len(rels[0].xs.size[2]));
+  w.first2 = c.take<int>(2 * rels[0].xs.size[0]);
   w.nl_s = c.take<float>(prows);
   w.nl_t = c.take<float>(prows);
   if (bytes != nullptr) *bytes = loss_bytes + c.bytes();
@@ -375,7 +383,7 @@ int check_batch(const lard_relation* rels, int nrel, const lard_mask* mask, floa
 }
 
 lard::HotArgs relation_args(const lard_relation& R, const lard_mask* mask, int causal, float sm_scale_s,
-                            float sm_scale_t, int Tp, const unsigned char* tok_ok) {
+                            float sm_scale_t, int Tp, const unsigned char* tok_ok, const int* first2) {
   lard::HotArgs f{};
   const int64_t H = R.xs.size[1];
   fill_side(f.r.s, &R.xs, &R.xs, H, sm_scale_s);
@@ -383,6 +391,7 @@ lard::HotArgs relation_args(const lard_relation& R, const lard_mask* mask, int c
   fill_common(f.r, R.xs.size[0], H, R.xs.size[2], mask, causal);
   f.Tp = Tp;
   f.tok_ok = tok_ok;
+  f.first2 = first2;
   return f;
 }
 
@@ -624,7 +633,8 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
         if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
         f.Tp = (int)padded_len(T);
         f.tok_ok = w.tok_ok;
-        if ((rc = hip_status(lard::launch_token_prep(f.r, f.Tp, w.tok_ok, st),
+        f.first2 = w.first2;
+        if ((rc = hip_status(lard::launch_token_prep(f.r, f.Tp, w.tok_ok, w.first2, st),
                              "attn_kl_forward token prep launch")) != LARD_OK)
           return rc;
         rc = hip_status(timed(LARD_KERNEL_FORWARD, st, [&] { return lard::launch_hot_fwd(f, padded_dim(ds), bf, st); }),
@@ -720,16 +730,17 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
     if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
     const int Tp = (int)padded_len(T);
     const BwdWs w = bwd_layout(workspace, B, Hq, T, nullptr);
-    if ((rc = hip_status(lard::launch_token_prep(a, Tp, w.tok_ok, st),
+    if ((rc = hip_status(lard::launch_token_prep(a, Tp, w.tok_ok, w.first2, st),
                          "attn_kl_backward token prep launch")) != LARD_OK)
       return rc;
-    if ((rc = hip_status(lard::launch_row_prep(a, Tp, w.tok_ok, w.nl_s, w.nl_t, st),
+    if ((rc = hip_status(lard::launch_row_prep(a, Tp, w.tok_ok, w.first2, w.nl_s, w.nl_t, st),
                          "attn_kl_backward row prep launch")) != LARD_OK)
       return rc;
     lard::HotArgs f{};
     f.r = a;
     f.Tp = Tp;
     f.tok_ok = w.tok_ok;
+    f.first2 = w.first2;
     f.nl_s = w.nl_s;
     f.nl_t = w.nl_t;
     f.dq_out = dq_dst;
@@ -771,8 +782,6 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                     "attn_kl_backward dk launch");
 }
 
-}  // extern "C"
-
 size_t lard_attn_kl_batched_workspace_bytes(const lard_relation* rels, int nrel) {
   if (rels == nullptr || nrel < 1) return 0;
   size_t bytes = 0;
@@ -803,8 +812,9 @@ int lard_attn_kl_batched_forward(const lard_relation* rels, int nrel, const lard
   const int dp = padded_dim(rels[0].xs.size[3]);
   const bool bf = rels[0].xs.dtype == LARD_DTYPE_BF16;
   {
-    const lard::HotArgs f0 = relation_args(rels[0], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok);
-    if ((rc = hip_status(lard::launch_token_prep(f0.r, Tp, w.tok_ok, st), "batched forward token prep launch")) !=
+    const lard::HotArgs f0 = relation_args(rels[0], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok, w.first2);
+    if ((rc = hip_status(lard::launch_token_prep(f0.r, Tp, w.tok_ok, w.first2, st),
+                         "batched forward token prep launch")) !=
         LARD_OK)
       return rc;
   }
@@ -813,7 +823,7 @@ int lard_attn_kl_batched_forward(const lard_relation* rels, int nrel, const lard
     lard::HotBatch m{};
     for (int r = g; r < nrel && r < g + lard::kMaxRelations; ++r) {
       if (rel_rows(rels[r]) == 0) continue;
-      lard::HotArgs f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok);
+      lard::HotArgs f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok, w.first2);
       f.lse_s_out = rels[r].lse_s;
       f.lse_t_out = rels[r].lse_t;
       f.row_out = w.loss.rows + row_off;
@@ -854,7 +864,7 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
   int64_t nl_off = 0;
   for (int r = 0; r < nrel; ++r) {
     lard::HotArgs& f = fs[(size_t)r];
-    f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok);
+    f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok, w.first2);
     f.r.lse_s_in = rels[r].lse_s;
     f.r.lse_t_in = rels[r].lse_t;
     float* nl_s = w.nl_s + nl_off;
@@ -862,10 +872,11 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
     f.nl_s = nl_s;
     f.nl_t = nl_t;
     nl_off += rels[r].xs.size[0] * rels[r].xs.size[1] * (int64_t)Tp;
-    if (r == 0 && (rc = hip_status(lard::launch_token_prep(f.r, Tp, w.tok_ok, st),
+    if (r == 0 && (rc = hip_status(lard::launch_token_prep(f.r, Tp, w.tok_ok, w.first2, st),
                                    "batched backward token prep launch")) != LARD_OK)
       return rc;
-    if (rel_rows(rels[r]) > 0 && (rc = hip_status(lard::launch_row_prep(f.r, Tp, w.tok_ok, nl_s, nl_t, st),
+    if (rel_rows(rels[r]) > 0 &&
+        (rc = hip_status(lard::launch_row_prep(f.r, Tp, w.tok_ok, w.first2, nl_s, nl_t, st),
                                                   "batched backward row prep launch")) != LARD_OK)
       return rc;
   }
@@ -895,7 +906,7 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
   return ok();
 }
 
-int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s,
+int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* inv_freq_s, float att_t, float att_s,
                    const int64_t* position_ids, int64_t pos_stride_b, void* out_t, void* out_s, void* stream) {
   int rc;
   if ((rc = check_tensor(x, "x")) != LARD_OK) return rc;
@@ -907,6 +918,8 @@ int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* 
     return fail(LARD_ERR_INVALID_ARGUMENT, "inv_freq and outputs must not be NULL");
   if (B * T * (D / 16) > (int64_t)INT32_MAX * 256)
     return fail(LARD_ERR_UNSUPPORTED, "rope_pair grid too large");
+  if (!std::isfinite(att_t) || !std::isfinite(att_s))
+    return fail(LARD_ERR_INVALID_ARGUMENT, "att_t / att_s must be finite");
   lard::RopeArgs a{};
   a.x = static_cast<const lard::u16*>(x->data);
   a.sb = x->stride[0];
@@ -918,6 +931,8 @@ int lard_rope_pair(const lard_tensor4* x, const float* inv_freq_t, const float* 
   a.D = (int)D;
   a.inv_freq_t = inv_freq_t;
   a.inv_freq_s = inv_freq_s;
+  a.att_t = att_t;
+  a.att_s = att_s;
   a.pos = position_ids;
   a.pos_sb = pos_stride_b;
   a.out_t = static_cast<lard::u16*>(out_t);
@@ -995,3 +1010,5 @@ int lard_logits_kl_backward(const lard_logits* t_logits, const lard_logits* s_lo
   return hip_status(timed(LARD_KERNEL_LOGITS_GRAD, st, [&] { return lard::launch_logits_kl_grad(a, t_logits->dtype, st); }),
                     "logits_kl backward launch");
 }
+
+}  // extern "C"

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
   // Online state (natural-log units; x = rounded dot * sm_scale).
   float m_s = kNegInf, l_s = 0.f;
   float m_t = kNegInf, l_t = 0.f;
-  float a_t = 0.f;  // sum_j p_t (x_t - x_s), same scaling as l_t
+  float a_t = 0.f;  // sum_j p_t ((x_t - m_t) - (x_s - m_s)), same scaling as l_t
 
   const int hs = h / a.s.group;
   const int ht = h / a.t.group;
@@ -117,6 +117,11 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
     const float mn_t = fmaxf(m_t, mb_t);
     const float c_s = (m_s == kNegInf) ? 0.f : fast_exp2((m_s - mn_s) * kLog2e);
     const float c_t = (m_t == kNegInf) ? 0.f : fast_exp2((m_t - mn_t) * kLog2e);
+    // terms of a_t are relative to the maxima: moving them to the new maxima
+    // adds (mn_s - m_s) - (mn_t - m_t) to each (both maxima are finite
+    // together: every valid element is valid on both sides)
+    const float shift = (m_t == kNegInf) ? 0.f : (mn_s - m_s) - (mn_t - m_t);
+    a_t = c_t * fmaf(l_t, shift, a_t);
     m_s = mn_s;
     m_t = mn_t;
 
@@ -128,14 +133,14 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
       pt[r] = valid[r] ? fast_exp2((xt[r] - mn_t) * kLog2e) : 0.f;
       sum_s += ps[r];
       sum_t += pt[r];
-      sum_a += valid[r] ? pt[r] * (xt[r] - xs[r]) : 0.f;
+      sum_a += valid[r] ? pt[r] * ((xt[r] - mn_t) - (xs[r] - mn_s)) : 0.f;
     }
     sum_s += xor32(sum_s);
     sum_t += xor32(sum_t);
     sum_a += xor32(sum_a);
     l_s = l_s * c_s + sum_s;
     l_t = l_t * c_t + sum_t;
-    a_t = a_t * c_t + sum_a;
+    a_t += sum_a;
   }
 
   const bool ok = row_valid && l_s > 0.f && l_t > 0.f;
@@ -145,10 +150,10 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
   if (in_range && half == 0) {
     f.lse_s_out[row_index] = row_valid ? lse_s : 0.f;  // kernel_A.py:157-158
     f.lse_t_out[row_index] = row_valid ? lse_t : 0.f;
-    // KL = E_pt[x_t - x_s] - lse_t + lse_s with lse = m + ln(l), regrouped so
-    // that no two rounded LSE values are subtracted: the max difference is
-    // exact for close maxima and the log ratio keeps its relative precision.
-    f.row_out[row_index] = ok ? a_t / l_t + (m_s - m_t) + (fast_log2(l_s) - fast_log2(l_t)) * kLn2 : 0.f;
+    // KL = E_pt[(x_t - m_t) - (x_s - m_s)] + ln(l_s / l_t) with lse = m + ln(l):
+    // max-relative terms only, so a row dominated by one key loses nothing to
+    // cancellation and a one-key row gives exactly 0 (its terms are 0 - 0 and ln 1).
+    f.row_out[row_index] = ok ? a_t / l_t + (fast_log2(l_s) - fast_log2(l_t)) * kLn2 : 0.f;
   }
 }
 

@@ -47,6 +47,7 @@ struct HotArgs {
   RelArgs r;
   int Tp;                        // T rounded up to kTile
   const unsigned char* tok_ok;   // [B][Tp] token validity
+  const int* first2;             // [B][2] first and second valid token of each sequence (T if none)
   const float* nl_s;             // backward: [B*Hq][Tp] -lse_s*log2(e), -inf for excluded rows
   const float* nl_t;
   float* lse_s_out;              // fwd: [B, Hq, T]
@@ -218,11 +219,16 @@ constexpr float kMaskedLogit = -1e30f;  // raw logit of a masked element
 constexpr float kStartMax = -5e29f;     // running max before the first valid key
 
 // Online-softmax state of one query row for this lane's half of the keys.
+// The exponent argument of a logit s is x = fma(s, c2, nm), its log2-domain
+// value relative to the stabiliser -nm; the KL term accumulates
+// p_t * (x_t - x_s), a difference of max-relative values, so a row dominated
+// by one key (logits far above the rest) loses nothing to cancellation, and
+// identical relations give exactly 0.
 struct SoftRow {
   float m_s, m_t;    // running maxima, raw (sign-corrected) logit units
   float nm_s, nm_t;  // -m * c2 (log2 units)
-  float l_s, l_t;    // sums of exp2(x * c2 + nm)
-  float acc;         // sum of p_t * (ratio * st - ss)
+  float l_s, l_t;    // sums of exp2(x_s), exp2(x_t)
+  float acc;         // sum of exp2(x_t) * (x_t - x_s)
 };
 
 // Set the invalid elements of a masked sub-block to kMaskedLogit.  Element r
@@ -240,24 +246,43 @@ __device__ __forceinline__ void mask_block(f32x16& ss, f32x16& st, unsigned bits
 
 // Partial sums of one sub-block against the running maxima.
 struct BlockSums {
-  float s, t, a;  // sum p_s, sum p_t, sum p_t * (ratio * st - ss)   (unnormalised)
+  float s, t, a;  // sum p_s, sum p_t, sum p_t * (x_t - x_s)   (unnormalised)
 };
 
 __device__ __forceinline__ BlockSums block_sums(const f32x16& ss, const f32x16& st, const SoftRow& R, float c2s,
-                                                float c2t, float ratio) {
+                                                float c2t) {
   float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; r += 2) {
-    const float pt0 = fast_exp2(fmaf(st[r], c2t, R.nm_t));
-    const float pt1 = fast_exp2(fmaf(st[r + 1], c2t, R.nm_t));
-    s0 += fast_exp2(fmaf(ss[r], c2s, R.nm_s));
-    s1 += fast_exp2(fmaf(ss[r + 1], c2s, R.nm_s));
+    const float xt0 = fmaf(st[r], c2t, R.nm_t), xt1 = fmaf(st[r + 1], c2t, R.nm_t);
+    const float xs0 = fmaf(ss[r], c2s, R.nm_s), xs1 = fmaf(ss[r + 1], c2s, R.nm_s);
+    const float pt0 = fast_exp2(xt0), pt1 = fast_exp2(xt1);
+    s0 += fast_exp2(xs0);
+    s1 += fast_exp2(xs1);
     t0 += pt0;
     t1 += pt1;
-    a0 = fmaf(pt0, fmaf(st[r], ratio, -ss[r]), a0);
-    a1 = fmaf(pt1, fmaf(st[r + 1], ratio, -ss[r + 1]), a1);
+    a0 = fmaf(pt0, xt0 - xs0, a0);
+    a1 = fmaf(pt1, xt1 - xs1, a1);
   }
   return {s0 + s1, t0 + t1, a0 + a1};
+}
+
+// Stabiliser -m * c2 of a running maximum m, as a rounded product the
+// compiler may not fuse into a later subtraction: two equal maxima must give
+// stabilisers whose difference is exactly 0 (a fused fma(-m, c2, -nm) would
+// leave the product's rounding error, ~1e21 for the start value kStartMax).
+__device__ __forceinline__ float stabiliser(float m, float c2) { return mul_rn(-m, c2); }
+
+// Move a lane's sums from the stabilisers (nm_s, nm_t) to (ns, nt) (log2
+// units, ns <= nm_s and nt <= nm_t): every exponent argument x drops by
+// nm - n, so the sums scale by exp2(n - nm) and each x_t - x_s term gains
+// (nt - nm_t) - (ns - nm_s).  With no term yet (l_t == 0) acc stays 0.
+__device__ __forceinline__ void restabilise(float& l_s, float& l_t, float& acc, float nm_s, float nm_t, float ns,
+                                            float nt) {
+  const float cs = fast_exp2(ns - nm_s), ct = fast_exp2(nt - nm_t);
+  acc = ct * fmaf(l_t, (nt - nm_t) - (ns - nm_s), acc);
+  l_s *= cs;
+  l_t *= ct;
 }
 
 // Raise the running maxima to the sub-block's maxima where those are larger,
@@ -269,16 +294,13 @@ __device__ __forceinline__ void raise_max(const f32x16& ss, const f32x16& st, So
     mb_s = fmaxf(fmaxf(mb_s, ss[r]), ss[r + 1]);
     mb_t = fmaxf(fmaxf(mb_t, st[r]), st[r + 1]);
   }
-  const float ns = fmaxf(mb_s, R.m_s), nt = fmaxf(mb_t, R.m_t);
-  const float cs = fast_exp2((R.m_s - ns) * c2s);
-  const float ct = fast_exp2((R.m_t - nt) * c2t);
-  R.m_s = ns;
-  R.m_t = nt;
-  R.nm_s = -ns * c2s;
-  R.nm_t = -nt * c2t;
-  R.l_s *= cs;
-  R.l_t *= ct;
-  R.acc *= ct;
+  const float ms = fmaxf(mb_s, R.m_s), mt = fmaxf(mb_t, R.m_t);
+  const float ns = stabiliser(ms, c2s), nt = stabiliser(mt, c2t);
+  restabilise(R.l_s, R.l_t, R.acc, R.nm_s, R.nm_t, ns, nt);
+  R.m_s = ms;
+  R.m_t = mt;
+  R.nm_s = ns;
+  R.nm_t = nt;
 }
 
 // Lazy maxima, checked on the sums: a lane's sub-block sums stay below
@@ -293,10 +315,10 @@ __device__ __forceinline__ void raise_max(const f32x16& ss, const f32x16& st, So
 constexpr float kLazySum = 1048576.f;  // 2^20
 
 __device__ __forceinline__ void add_block(const f32x16& ss, const f32x16& st, BlockSums bs, SoftRow& R, float c2s,
-                                          float c2t, float ratio) {
+                                          float c2t) {
   if (__any(!(bs.s <= kLazySum) || !(bs.t <= kLazySum))) {
     raise_max(ss, st, R, c2s, c2t);
-    bs = block_sums(ss, st, R, c2s, c2t, ratio);
+    bs = block_sums(ss, st, R, c2s, c2t);
   }
   R.l_s += bs.s;
   R.l_t += bs.t;
@@ -334,7 +356,7 @@ template <int DP, bool BF, int PD = 2, bool PRE_IN = false, bool PRE_OUT = false
 __device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int half,
                                                      const u16x8* fq_s, const u16x8* fq_t, f32x16& ns, f32x16& nt,
                                                      const f32x16& ss, const f32x16& st, const SoftRow& R, float c2s,
-                                                     float c2t, float ratio, u16x8* pre = nullptr, int pre_row = 0) {
+                                                     float c2t, u16x8* pre = nullptr, int pre_row = 0) {
   constexpr int KS = DP / 16, EP = 16 / KS;
   u16x8 os[KS], ot[KS];
   auto load = [&](int kk) {
@@ -371,8 +393,8 @@ __device__ __forceinline__ BlockSums scores_and_sums(const u16* ks, int row, int
       // back, then the sums: no fma -> exp -> add dependency at issue
       float xt0 = fmaf(st[r], c2t, R.nm_t), xt1 = fmaf(st[r + 1], c2t, R.nm_t);
       float xs0 = fmaf(ss[r], c2s, R.nm_s), xs1 = fmaf(ss[r + 1], c2s, R.nm_s);
-      const float d0 = fmaf(st[r], ratio, -ss[r]), d1 = fmaf(st[r + 1], ratio, -ss[r + 1]);
       asm volatile("" : "+v"(xt0), "+v"(xt1), "+v"(xs0), "+v"(xs1));
+      const float d0 = xt0 - xs0, d1 = xt1 - xs1;
       const float pt0 = fast_exp2(xt0), pt1 = fast_exp2(xt1);
       const float ps0 = fast_exp2(xs0), ps1 = fast_exp2(xs1);
       s0 += ps0;
@@ -436,8 +458,7 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   }
 
   const float c2s = fabsf(a.s.scale2), c2t = fabsf(a.t.scale2);  // raw logit -> log2 units
-  const float ratio = c2t / c2s;                                 // x_t - x_s = c2s * (ratio*st - ss)
-  SoftRow R = {kStartMax, kStartMax, -kStartMax * c2s, -kStartMax * c2t, 0.f, 0.f, 0.f};
+  SoftRow R = {kStartMax, kStartMax, stabiliser(kStartMax, c2s), stabiliser(kStartMax, c2t), 0.f, 0.f, 0.f};
 
   const int hs = h / a.s.group, ht = h / a.t.group;
   const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
@@ -493,15 +514,15 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
     BlockSums bs;
     if (sb2 == 0)
       bs = scores_and_sums<DP, BF, 2, false, true>(lk[buf][0], l32, half, fq_s, fq_t, nxt.s, nxt.t, cur.s, cur.t, R,
-                                                   c2s, c2t, ratio, pre, 32 + l32);
+                                                   c2s, c2t, pre, 32 + l32);
     else
       bs = scores_and_sums<DP, BF, 2, true, false>(lk[buf][0], 32 + l32, half, fq_s, fq_t, nxt.s, nxt.t, cur.s,
-                                                   cur.t, R, c2s, c2t, ratio, pre);
-    add_block(cur.s, cur.t, bs, R, c2s, c2t, ratio);
+                                                   cur.t, R, c2s, c2t, pre);
+    add_block(cur.s, cur.t, bs, R, c2s, c2t);
   };
   auto last = [&](Sub& cur, int it, int sb) {
     prepare(cur, it, sb);
-    add_block(cur.s, cur.t, block_sums(cur.s, cur.t, R, c2s, c2t, ratio), R, c2s, c2t, ratio);
+    add_block(cur.s, cur.t, block_sums(cur.s, cur.t, R, c2s, c2t), R, c2s, c2t);
   };
 
   // The register operands loaded above must have landed before the ring
@@ -546,23 +567,31 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
     }
   }
 
-  // merge the two halves of the row: common maxima, rescaled sums
+  // merge the two halves of the row: common maxima (the larger half keeps
+  // its stabilisers exactly), sums moved to them
   const float ms = fmaxf(R.m_s, xor32(R.m_s)), mt = fmaxf(R.m_t, xor32(R.m_t));
-  const float fs = fast_exp2((R.m_s - ms) * c2s), ft = fast_exp2((R.m_t - mt) * c2t);
-  const float ls_h = R.l_s * fs, lt_h = R.l_t * ft, acc_h = R.acc * ft;
-  const float l_s = ls_h + xor32(ls_h);
-  const float l_t = lt_h + xor32(lt_h);
-  const float acc = acc_h + xor32(acc_h);
+  const float ns = stabiliser(ms, c2s), nt = stabiliser(mt, c2t);
+  restabilise(R.l_s, R.l_t, R.acc, R.nm_s, R.nm_t, ns, nt);
+  const float l_s = R.l_s + xor32(R.l_s);
+  const float l_t = R.l_t + xor32(R.l_t);
+  const float acc = R.acc + xor32(R.acc);
   const bool ok = row_valid && l_s > 0.f && l_t > 0.f;
   const float lg_s = fast_log2(l_s), lg_t = fast_log2(l_t);
-  const float xs = ms * c2s, xt = mt * c2t;  // row maxima, log2 units
+  // A valid row with exactly one valid key (the first valid token of a
+  // causal row; the only valid token otherwise) has P_s = P_t = 1 there: its
+  // KL is exactly 0 and its LSE is the logit itself, rounded once as the
+  // reference rounds S = dot * sm_scale (kernel_A.py:147-157, kernel_B.py:206-213).
+  const bool one_key = row_valid && (causal ? my_i == f.first2[2 * b] : f.first2[2 * b + 1] >= T);
   const int64_t row_index = (int64_t)bh * T + my_i;
   if (in_range && half == 0) {
-    f.lse_s_out[row_index] = row_valid ? (l_s > 0.f ? (xs + lg_s) * kLn2 : kNegInf) : 0.f;
-    f.lse_t_out[row_index] = row_valid ? (l_t > 0.f ? (xt + lg_t) * kLn2 : kNegInf) : 0.f;
-    // KL = E_pt[x_t - x_s] + (max_s - max_t) + ln(l_s / l_t); no two rounded LSEs are subtracted
+    const float ls = one_key ? mul_rn(ms, fabsf(a.s.scale)) : (l_s > 0.f ? (lg_s - ns) * kLn2 : kNegInf);
+    const float lt = one_key ? mul_rn(mt, fabsf(a.t.scale)) : (l_t > 0.f ? (lg_t - nt) * kLn2 : kNegInf);
+    f.lse_s_out[row_index] = row_valid ? ls : 0.f;
+    f.lse_t_out[row_index] = row_valid ? lt : 0.f;
+    // KL = E_pt[x_t - x_s] + ln(l_s / l_t): max-relative terms only, no two
+    // rounded LSEs or maxima are subtracted
     const float wr = a.weight != nullptr ? *a.weight : 1.f;
-    f.row_out[row_index] = ok ? (acc * c2s / l_t + (xs - xt) + (lg_s - lg_t)) * kLn2 * wr : 0.f;
+    f.row_out[row_index] = ok && !one_key ? (acc / l_t + (lg_s - lg_t)) * kLn2 * wr : 0.f;
   }
 }
 
@@ -1129,9 +1158,9 @@ __global__ __launch_bounds__(kWaves * 64) void hot_bwd_batch_kernel(const HotBat
 }
 
 bool hot_supported(int ds, int dt, bool same_dtype);
-hipError_t launch_token_prep(const RelArgs& a, int Tp, unsigned char* tok_ok, hipStream_t stream);
-hipError_t launch_row_prep(const RelArgs& a, int Tp, const unsigned char* tok_ok, float* nl_s, float* nl_t,
-                           hipStream_t stream);
+hipError_t launch_token_prep(const RelArgs& a, int Tp, unsigned char* tok_ok, int* first2, hipStream_t stream);
+hipError_t launch_row_prep(const RelArgs& a, int Tp, const unsigned char* tok_ok, const int* first2, float* nl_s,
+                           float* nl_t, hipStream_t stream);
 hipError_t launch_hot_fwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
 hipError_t launch_hot_dq(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
 hipError_t launch_hot_bwd(const HotArgs& f, int dp, bool bf16, hipStream_t stream);

@@ -7,7 +7,9 @@
 // writes both rotated tensors, contiguous [B, H, T, D], with HF's arithmetic:
 //
 //   angle = pos * inv_freq[i]                  (float32, one rounding)
-//   c, s  = cos(angle), sin(angle) rounded to the input dtype
+//   c, s  = cos(angle) * att, sin(angle) * att rounded to the input dtype
+//           (att: HF's attention_scaling of the rope type, a float32 product;
+//           1 for default / linear / dynamic / llama3, which changes nothing)
 //   out[i]       = R(R(x[i] * c) + R(-x[i + D/2] * s))       i < D/2
 //   out[i + D/2] = R(R(x[i + D/2] * c) + R(x[i] * s))
 //
@@ -59,10 +61,10 @@ __global__ __launch_bounds__(256) void rope_pair_kernel(const RopeArgs a) {
   for (int e = 0; e < 8; ++e) {
     const float at = p * a.inv_freq_t[8 * c + e];
     const float as = p * a.inv_freq_s[8 * c + e];
-    ct[e] = round_to_input<BF>(cosf(at));
-    sn_t[e] = round_to_input<BF>(sinf(at));
-    cs[e] = round_to_input<BF>(cosf(as));
-    sn_s[e] = round_to_input<BF>(sinf(as));
+    ct[e] = round_to_input<BF>(cosf(at) * a.att_t);
+    sn_t[e] = round_to_input<BF>(sinf(at) * a.att_t);
+    cs[e] = round_to_input<BF>(cosf(as) * a.att_s);
+    sn_s[e] = round_to_input<BF>(sinf(as) * a.att_s);
   }
   const int half = a.D / 2;
   const u16* xb = a.x + (int64_t)b * a.sb + (int64_t)t * a.st + 8 * c;

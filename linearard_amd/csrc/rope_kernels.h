@@ -11,6 +11,7 @@ struct RopeArgs {
   int B, H, T, D;
   const float* inv_freq_t;  // [D/2] teacher
   const float* inv_freq_s;  // [D/2] student
+  float att_t, att_s;       // cos / sin multipliers (HF's attention_scaling; 1 for most rope types)
   const int64_t* pos;       // [B, T] position ids, or null for 0..T-1
   int64_t pos_sb;
   u16* out_t;               // [B, H, T, D] contiguous

@@ -9,7 +9,9 @@ at train.py:116-142 capturing the rotated tensors):
 
 * angles ``pos * inv_freq[i]`` as one float32 product (HF's float32
   ``inv_freq @ position_ids``), ``emb = cat(freqs, freqs)``;
-* ``cos``, ``sin`` of the angles, cast to the tensor dtype;
+* ``cos``, ``sin`` of the angles times the rope type's attention scaling (a
+  float32 product; HF's ``emb.cos() * attention_scaling``), cast to the
+  tensor dtype;
 * ``q * cos + rotate_half(q) * sin`` in the tensor dtype, rotate_half =
   ``cat(-x2, x1)``: every product and the sum rounded to the dtype (bf16
   tensor arithmetic rounds each operation's float32 result).
@@ -30,17 +32,19 @@ from .attn_kl import round_to
 __all__ = ["rope_apply"]
 
 
-def rope_apply(x, inv_freq, positions, dtype):
+def rope_apply(x, inv_freq, positions, dtype, attention_scaling=1.0):
     """x: [..., T, D] float32 values of the dtype; inv_freq: float32 [D/2];
-    positions: [T] (or broadcastable [..., T]) integer positions.  Returns the
-    rotated tensor as float32 values of the dtype."""
+    positions: [T] (or broadcastable [..., T]) integer positions;
+    attention_scaling: the cos / sin multiplier.  Returns the rotated tensor
+    as float32 values of the dtype."""
     x = np.asarray(x, dtype=np.float32)
     D = x.shape[-1]
     half = D // 2
     pos = np.asarray(positions).astype(np.float32)
     ang = (pos[..., :, None] * np.asarray(inv_freq, dtype=np.float32)[None, :]).astype(np.float32)
-    c = round_to(np.cos(ang.astype(np.float64)).astype(np.float32), dtype)
-    s = round_to(np.sin(ang.astype(np.float64)).astype(np.float32), dtype)
+    att = np.float32(attention_scaling)
+    c = round_to((np.cos(ang.astype(np.float64)).astype(np.float32) * att).astype(np.float32), dtype)
+    s = round_to((np.sin(ang.astype(np.float64)).astype(np.float32) * att).astype(np.float32), dtype)
     x1, x2 = x[..., :half], x[..., half:]
     o1 = round_to(round_to(x1 * c, dtype) + round_to(-x2 * s, dtype), dtype)
     o2 = round_to(round_to(x2 * c, dtype) + round_to(x1 * s, dtype), dtype)

@@ -59,13 +59,15 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert L.lard_kl_forward_workspace_bytes(2, 3, 5) == 256 + 512 * 8
     assert L.lard_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8
     assert L.lard_kl_forward_workspace_bytes(0, 3, 5) == 0
-    # forward of the autograd path adds one validity byte per (padded) token
-    assert L.lard_attn_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8 + 4 * 4096
-    # backward: validity bytes and 2 normalisers per (padded) row, or, when
-    # larger, the float32 path's two double LSEs per row
+    # forward of the autograd path adds one validity byte per (padded) token and
+    # the first two valid tokens of each sequence (two int32, 256-aligned)
+    assert L.lard_attn_kl_forward_workspace_bytes(4, 32, 4096) == 4 * 32 * 4096 * 4 + 512 * 8 + 4 * 4096 + 256
+    # backward: validity bytes, the first two valid tokens per sequence and 2
+    # normalisers per (padded) row, or, when larger, the float32 path's two
+    # double LSEs per row
     B, H, T, D = 2, 8, 1000, 64
     Tp = 1024
-    tail = B * Tp + 2 * B * H * Tp * 4
+    tail = B * Tp + 256 + 2 * B * H * Tp * 4
     f64 = (2 * B * H * T * 8 + 255) // 256 * 256
     assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 1) == max(tail, f64)
     assert L.lard_attn_kl_backward_workspace_bytes(B, H, H, T, D, 0) == max(tail, f64)
@@ -84,9 +86,10 @@ def test_batched_abi_rejects_bad_batches_without_a_gpu():
         rels[r].lse_s = rels[r].lse_t = rels[r].dxs = 512
     m = _lib.Mask()
     ws = L.lard_attn_kl_batched_workspace_bytes(rels, 2)
-    # rows of both relations (KL terms, 256-aligned) + loss partials + validity bytes + two normalisers per row
+    # rows of both relations (KL terms, 256-aligned) + loss partials + validity
+    # bytes + first two valid tokens + two normalisers per row
     rows = 1 * (4 + 2) * 64
-    assert ws == rows * 4 + 512 * 8 + 256 + 2 * rows * 4
+    assert ws == rows * 4 + 512 * 8 + 256 + 256 + 2 * rows * 4
     assert L.lard_attn_kl_batched_workspace_bytes(None, 0) == 0
     rc = L.lard_attn_kl_batched_forward(rels, 0, ctypes.byref(m), 1, 0.1, 0.1, None, 1024, None, 0, None)
     assert rc == -1 and b"at least one relation" in L.lard_last_error()
@@ -111,12 +114,14 @@ def test_rope_abi_rejects_bad_arguments_without_a_gpu():
     t.size[:] = [1, 2, 16, 8]
     t.stride[:] = [256, 128, 8, 1]
     t.dtype = 1
-    rc = L.lard_rope_pair(ctypes.byref(t), 512, 512, None, 0, 1024, 2048, None)
+    rc = L.lard_rope_pair(ctypes.byref(t), 512, 512, 1.0, 1.0, None, 0, 1024, 2048, None)
     assert rc == -2 and b"multiple of 16" in L.lard_last_error()
     t.size[3] = 64
     t.stride[:] = [2048, 1024, 64, 1]
-    rc = L.lard_rope_pair(ctypes.byref(t), None, 512, None, 0, 1024, 2048, None)
+    rc = L.lard_rope_pair(ctypes.byref(t), None, 512, 1.0, 1.0, None, 0, 1024, 2048, None)
     assert rc == -1 and b"must not be NULL" in L.lard_last_error()
+    rc = L.lard_rope_pair(ctypes.byref(t), 512, 512, 1.0, float("nan"), None, 0, 1024, 2048, None)
+    assert rc == -1 and b"finite" in L.lard_last_error()
 
 
 def _logits_desc(B=1, K=4, V=64, dtype=1, data=4096):

@@ -72,3 +72,32 @@ def test_rope_pair_rejects_unsupported_head_dims(gpu_available):
     x = torch.zeros((1, 1, 8, 8), device="cuda", dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="multiple of 16"):
         rope_pair(x, 1e4)
+
+
+@pytest.mark.parametrize("dtype,scaling,student_base,max_pos", [
+    ("bf16", None, 5e5 * 8, None),  # cfg3: teacher base 5e5, NTK student base x 8
+    ("bf16", {"rope_type": "yarn", "factor": 8.0, "original_max_position_embeddings": 1024}, None, None),
+    ("f16", {"rope_type": "dynamic", "factor": 4.0}, None, 256),
+    ("bf16", {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+              "original_max_position_embeddings": 256}, None, None),
+])
+def test_rope_pair_other_rope_types_match_oracle(gpu_available, dtype, scaling, student_base, max_pos):
+    """Every HF rope type the student of train.py:206-213 may use: the
+    producer's student equals the oracle's rotation with rope_parameters'
+    frequencies and attention scaling; the teacher keeps the native base."""
+    from linearard_amd.rope import rope_pair, rope_parameters
+
+    B, H, T, D = 1, 3, 700, 128
+    base = 5e5
+    rng = np.random.default_rng(17)
+    x = round_to(rng.standard_normal((B, H, T, D)).astype(np.float32), dtype)
+    xd = torch.tensor(x, device="cuda").to(TD[dtype])
+    xs, xt = rope_pair(xd, base, scaling, student_base=student_base, max_position_embeddings=max_pos)
+    inv_t, att_t = rope_parameters(D, base)
+    inv_s, att_s = rope_parameters(D, student_base or base, scaling, max_position_embeddings=max_pos, seq_len=T)
+    pos = np.arange(T)
+    _check(xt[0], R.rope_apply(x[0], inv_t.numpy(), pos, dtype, att_t), x[0], dtype)
+    ref_s = R.rope_apply(x[0], inv_s.numpy(), pos, dtype, att_s)
+    _check(xs[0], ref_s, x[0], dtype)
+    if student_base is not None or att_s != 1.0:  # the student really differs from the teacher
+        assert not torch.equal(xs, xt)
