@@ -133,6 +133,29 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
                          float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the library's own forward workspace on each GPU (16 MiB), held
+ * from the first lard_attn_kl_forward_noalloc call on that GPU until the
+ * process ends. */
+#define LARD_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/*
+ * lard_attn_kl_forward without a workspace argument and without any device
+ * allocation: no counterpart in the reference.  It is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, outputs and results as
+ * lard_attn_kl_forward; the workspace is a library array of
+ * LARD_NOALLOC_SCRATCH_BYTES per GPU, so lard_attn_kl_forward_workspace_bytes(B,
+ * Hq, T) must not exceed it (about 4M rows B * Hq * T; cfg4's 1M rows fit),
+ * else LARD_ERR_UNSUPPORTED.  Every call on one GPU uses that GPU's array:
+ * calls that overlap on one GPU (other streams, other host threads) race;
+ * calls ordered on one stream do not.  Nothing in the array needs clearing:
+ * each call writes every byte it reads.
+ */
+int lard_attn_kl_forward_noalloc(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+                                 const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
+                                 float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
+                                 void* stream);
+
 /* Workspace needed by lard_attn_kl_backward (bytes): one validity byte per
  * token and two log2-domain row normalisers per query row.  kv_heads,
  * head_dim and self_relation do not change the size; they are kept so the

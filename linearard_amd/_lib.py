@@ -91,6 +91,8 @@ SIGNATURES = {
     "lard_attn_kl_forward": (ctypes.c_int, [_T4P, _T4P, _T4P, _T4P, _MP, ctypes.c_int, ctypes.c_float,
                                             ctypes.c_float, _FP, _FP, _FP, ctypes.c_void_p, ctypes.c_size_t,
                                             ctypes.c_void_p]),
+    "lard_attn_kl_forward_noalloc": (ctypes.c_int, [_T4P, _T4P, _T4P, _T4P, _MP, ctypes.c_int, ctypes.c_float,
+                                                    ctypes.c_float, _FP, _FP, _FP, ctypes.c_void_p]),
     "lard_attn_kl_backward_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 5 + [ctypes.c_int]),
     "lard_attn_kl_backward": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, _FP, ctypes.c_int, _FP, _FP, ctypes.c_void_p,

@@ -589,10 +589,18 @@ size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_
   return bytes;
 }
 
-int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+}  // extern "C"
+
+namespace {
+
+// The forward of lard_attn_kl_forward.  need_workspace(B, Hq, T) returns the
+// workspace to use once the shapes are checked: the caller's (checked
+// against its size), or the library's scratch array (lard_attn_kl_forward_noalloc).
+template <class NeedWorkspace>
+int attn_kl_forward_impl(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
                          const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
-                         float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+                         float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
+                         NeedWorkspace need_workspace, void* stream) {
   int rc;
   if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
   if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
@@ -611,9 +619,8 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
     if (lse_s_out == nullptr || lse_t_out == nullptr)
       return fail(LARD_ERR_INVALID_ARGUMENT, "lse outputs must not be NULL");
     if ((rc = check_grid(B * Hq)) != LARD_OK) return rc;
-    const size_t need = lard_attn_kl_forward_workspace_bytes(B, Hq, T);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+    void* workspace = nullptr;
+    if ((rc = need_workspace(B, Hq, T, &workspace)) != LARD_OK) return rc;
     const int ds = (int)qs->size[3], dt = (int)qt->size[3];
     const bool same = qs->dtype == qt->dtype;
     const bool bf = qs->dtype == LARD_DTYPE_BF16;
@@ -680,6 +687,83 @@ int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const l
                       "attn_kl_forward reduce launch");
   }
   return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "attn_kl_forward reduce launch");
+}
+
+// ---- the library's own forward workspace (lard_attn_kl_forward_noalloc) ----
+
+// One array per GPU, held until the process ends.  Host code never uses its
+// name as an address: each device's copy is reached through the pointer
+// hipGetSymbolAddress returns with that device current.
+constexpr size_t kScratchBytes = LARD_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device the work of `stream` runs on (the current device for the null stream).
+int stream_device(hipStream_t stream, int* dev) {
+  hipError_t e = stream != nullptr ? hipStreamGetDevice(stream, dev) : hipGetDevice(dev);
+  if (e != hipSuccess) return fail(LARD_ERR_HIP, "stream device: %s", hipGetErrorString(e));
+  if (*dev < 0 || *dev >= kMaxDevices) return fail(LARD_ERR_UNSUPPORTED, "device %d beyond %d", *dev, kMaxDevices);
+  return LARD_OK;
+}
+
+// This device's copy of `scratch`, looked up once per device with that device current.
+int scratch_on(int dev, void** out) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return fail(LARD_ERR_HIP, "scratch address on device %d: %s", dev, hipGetErrorString(e));
+    if (p == nullptr) return fail(LARD_ERR_HIP, "scratch address on device %d is NULL", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LARD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lard_attn_kl_forward(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+                         const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
+                         float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  auto caller_ws = [&](int64_t B, int64_t Hq, int64_t T, void** ws) {
+    const size_t need = lard_attn_kl_forward_workspace_bytes(B, Hq, T);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+    *ws = workspace;
+    return LARD_OK;
+  };
+  return attn_kl_forward_impl(qs, ks, qt, kt, mask, causal, sm_scale_s, sm_scale_t, lse_s_out, lse_t_out, loss_out,
+                              caller_ws, stream);
+}
+
+int lard_attn_kl_forward_noalloc(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+                                 const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
+                                 float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out, void* stream) {
+  auto library_ws = [&](int64_t B, int64_t Hq, int64_t T, void** ws) {
+    const size_t need = lard_attn_kl_forward_workspace_bytes(B, Hq, T);
+    if (need > kScratchBytes)
+      return fail(LARD_ERR_UNSUPPORTED, "forward needs %zu bytes of scratch; the library holds %zu per device "
+                                        "(B * Hq * T is too large for the no-allocation entry point)",
+                  need, kScratchBytes);
+    int dev = -1, rc;
+    if ((rc = stream_device(static_cast<hipStream_t>(stream), &dev)) != LARD_OK) return rc;
+    return scratch_on(dev, ws);
+  };
+  return attn_kl_forward_impl(qs, ks, qt, kt, mask, causal, sm_scale_s, sm_scale_t, lse_s_out, lse_t_out, loss_out,
+                              library_ws, stream);
 }
 
 size_t lard_attn_kl_backward_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq_len,

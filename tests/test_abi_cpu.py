@@ -74,6 +74,24 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert L.lard_attn_kl_backward_workspace_bytes(0, H, H, T, D, 0) == 0
 
 
+def test_noalloc_forward_rejects_sizes_beyond_its_scratch_without_a_gpu():
+    """The library's own workspace holds LARD_NOALLOC_SCRATCH_BYTES (16 MiB) per
+    GPU: a forward needing more is refused before anything is launched."""
+    L = _lib.lib()
+    t = _lib.Tensor4()
+    t.data = 256
+    B, H, T, D = 1, 64, 65536, 128  # 4M rows: 16 MiB of row KL terms alone
+    t.size[:] = [B, H, T, D]
+    t.stride[:] = [H * T * D, T * D, D, 1]
+    t.dtype = 1
+    m = _lib.Mask()
+    need = L.lard_attn_kl_forward_workspace_bytes(B, H, T)
+    assert need > 16 << 20
+    rc = L.lard_attn_kl_forward_noalloc(ctypes.byref(t), ctypes.byref(t), ctypes.byref(t), ctypes.byref(t),
+                                        ctypes.byref(m), 1, 0.1, 0.1, 512, 1024, 2048, None)
+    assert rc == -2 and b"scratch" in L.lard_last_error()
+
+
 def test_batched_abi_rejects_bad_batches_without_a_gpu():
     L = _lib.lib()
     rels = (_lib.Relation * 2)()
