@@ -117,6 +117,25 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
                      const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
                      float* dq_out, float* dk_out, void* stream);
 
+/* Kernels of the autograd calls (lard_attn_kl_forward / _backward), by operands. */
+#define LARD_PATH_THROUGHPUT 0     /* the throughput kernels: one-pass forward, row + column backward */
+#define LARD_PATH_FUSED_FORWARD 1  /* one-pass forward, stage-kernel backward (several times slower) */
+#define LARD_PATH_STAGE 2          /* stage kernels only: the reference's composition (about 6x slower) */
+#define LARD_PATH_FLOAT32 3        /* float32 inputs: the double-precision kernels */
+
+/*
+ * Which kernels lard_attn_kl_forward / lard_attn_kl_backward run for these
+ * operands: a LARD_PATH_* value (>= 0), or a negative error for invalid
+ * operands.  After a non-throughput answer, lard_last_error() names the
+ * condition (head dims differ or exceed 128, dtypes differ, a head of 2^30
+ * elements or more, scales outside [1e-6, 1e6] or more than 1e6 apart,
+ * float32); it is empty for LARD_PATH_THROUGHPUT.  No counterpart in the
+ * reference (one Triton path, kernel_A.py / kernel_B.py / kernel_C.py); it
+ * lets a caller see the slower paths the reference does not have.
+ */
+int lard_attn_kl_path(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt, const lard_tensor4* kt,
+                      float sm_scale_s, float sm_scale_t);
+
 /* Workspace needed by lard_attn_kl_forward (bytes): the per-row KL terms,
  * the loss-sum partials and one validity byte per token. */
 size_t lard_attn_kl_forward_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len);

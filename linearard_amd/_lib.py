@@ -81,6 +81,7 @@ _FP = ctypes.c_void_p  # float* device pointers are passed as addresses
 SIGNATURES = {
     "lard_version": (ctypes.c_char_p, []),
     "lard_last_error": (ctypes.c_char_p, []),
+    "lard_attn_kl_path": (ctypes.c_int, [_T4P, _T4P, _T4P, _T4P, ctypes.c_float, ctypes.c_float]),
     "lard_lse_stats": (ctypes.c_int, [_T4P, _T4P, _MP, ctypes.c_int, ctypes.c_float, _FP, ctypes.c_void_p]),
     "lard_kl_forward_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     "lard_kl_forward": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int, ctypes.c_float,

@@ -19,6 +19,7 @@ second input) instead of two float32 tensors for autograd to add.
 from __future__ import annotations
 
 import ctypes
+import warnings
 
 import torch
 
@@ -30,6 +31,29 @@ __all__ = ["AttnKLAlignFn", "attn_kl_align"]
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty((nbytes if nbytes > 0 else 1,), device=device, dtype=torch.uint8)
+
+
+PATH_NAMES = {0: "throughput", 1: "fused-forward", 2: "stage", 3: "float32"}
+_WARNED = set()
+
+
+def kernel_path(d, ss: float, st: float):
+    """(path name, condition) of lard_attn_kl_path for the four operand descriptors."""
+    L = _lib.lib()
+    rc = L.lard_attn_kl_path(ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), ctypes.byref(d[3]), ss, st)
+    if rc < 0:  # a path code otherwise, not a status
+        _lib.check(rc, "lard_attn_kl_path")
+    return PATH_NAMES[rc], L.lard_last_error().decode()
+
+
+def _warn_slow_path(d, ss: float, st: float) -> None:
+    """One RuntimeWarning per condition that moves a call off the throughput
+    kernels (the stage kernels are about 6x slower)."""
+    name, why = kernel_path(d, ss, st)
+    if name != "throughput" and why not in _WARNED:
+        _WARNED.add(why)
+        warnings.warn(f"attn_kl_align: {why}: these inputs run the {name} kernels, not the throughput "
+                      f"kernels (several times slower)", RuntimeWarning, stacklevel=3)
 
 
 class AttnKLAlignFn(torch.autograd.Function):
@@ -49,6 +73,8 @@ class AttnKLAlignFn(torch.autograd.Function):
         ws_bytes = L.lard_attn_kl_forward_workspace_bytes(B, Hq, T)
         ws = _workspace(ws_bytes, dev)
         d = [_lib.tensor4(x) for x in (qs, ks, qt, kt)]
+        if B * Hq * T > 0:
+            _warn_slow_path(d, ss, st)
         md = _lib.mask_desc(attn_mask)
         rc = L.lard_attn_kl_forward(ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), ctypes.byref(d[3]),
                                     ctypes.byref(md), int(bool(causal)), ss, st, lse_s.data_ptr(), lse_t.data_ptr(),

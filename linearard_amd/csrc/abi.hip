@@ -189,6 +189,40 @@ bool hot_scales_ok(float s, float t) {
   return as >= 1e-6f && at >= 1e-6f && as <= 1e6f && at <= 1e6f && as <= 1e6f * at && at <= 1e6f * as;
 }
 
+// The kernels an autograd call (lard_attn_kl_forward / _backward) runs for
+// these operands, and in `why` the condition that took it off the
+// throughput kernels (empty on them).  Checked operands only.
+int attn_kl_path(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt, const lard_tensor4* kt,
+                 float sm_scale_s, float sm_scale_t, std::string* why) {
+  const int ds = (int)qs->size[3], dt = (int)qt->size[3];
+  const bool same = qs->dtype == qt->dtype;
+  char buf[160];
+  if (qs->dtype == LARD_DTYPE_F32) {
+    *why = "float32 inputs run the double-precision kernels";
+    return LARD_PATH_FLOAT32;
+  }
+  if (!lard::hot_supported(ds, dt, same)) {
+    if (!same)
+      *why = "student and teacher dtypes differ";
+    else if (ds != dt)
+      snprintf(buf, sizeof(buf), "student head dim %d != teacher head dim %d", ds, dt), *why = buf;
+    else
+      snprintf(buf, sizeof(buf), "head dim %d > 128", ds), *why = buf;
+    return lard::fused_fwd_supported(ds, dt, same) ? LARD_PATH_FUSED_FORWARD : LARD_PATH_STAGE;
+  }
+  if (!hot_offsets_ok({qs, ks, qt, kt}, qs->size[2])) {
+    *why = "a head spans 2^30 elements or more (32-bit offsets)";
+    return LARD_PATH_FUSED_FORWARD;
+  }
+  if (!hot_scales_ok(sm_scale_s, sm_scale_t)) {
+    snprintf(buf, sizeof(buf), "scales %g / %g outside [1e-6, 1e6] or more than 1e6 apart", sm_scale_s, sm_scale_t);
+    *why = buf;
+    return LARD_PATH_FUSED_FORWARD;
+  }
+  why->clear();
+  return LARD_PATH_THROUGHPUT;
+}
+
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Carves 256-byte aligned regions out of a caller workspace in a fixed
@@ -502,6 +536,19 @@ const char* lard_version(void) { return "linearard_amd 0.1.0 gfx950"; }
 
 const char* lard_last_error(void) { return g_last_error.c_str(); }
 
+int lard_attn_kl_path(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt, const lard_tensor4* kt,
+                      float sm_scale_s, float sm_scale_t) {
+  int rc;
+  if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
+  if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_s, "sm_scale_s")) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_t, "sm_scale_t")) != LARD_OK) return rc;
+  std::string why;
+  const int path = attn_kl_path(qs, ks, qt, kt, sm_scale_s, sm_scale_t, &why);
+  g_last_error = why;
+  return path;
+}
+
 int lard_lse_stats(const lard_tensor4* q, const lard_tensor4* k, const lard_mask* mask, int causal, float sm_scale,
                    float* lse_out, void* stream) {
   int rc;
@@ -622,13 +669,13 @@ int attn_kl_forward_impl(const lard_tensor4* qs, const lard_tensor4* ks, const l
     void* workspace = nullptr;
     if ((rc = need_workspace(B, Hq, T, &workspace)) != LARD_OK) return rc;
     const int ds = (int)qs->size[3], dt = (int)qt->size[3];
-    const bool same = qs->dtype == qt->dtype;
     const bool bf = qs->dtype == LARD_DTYPE_BF16;
-    const bool f32 = qs->dtype == LARD_DTYPE_F32;  // float32 runs the stage kernels
     const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
-    const bool hot = !f32 && lard::hot_supported(ds, dt, same) && hot_offsets_ok({qs, ks, qt, kt}, T) &&
-                     hot_scales_ok(sm_scale_s, sm_scale_t);
-    if (hot || (!f32 && lard::fused_fwd_supported(ds, dt, same))) {
+    std::string why;
+    const int path = attn_kl_path(qs, ks, qt, kt, sm_scale_s, sm_scale_t, &why);
+    const bool hot = path == LARD_PATH_THROUGHPUT;
+    const bool f32 = path == LARD_PATH_FLOAT32;
+    if (hot || path == LARD_PATH_FUSED_FORWARD) {
       lard::HotArgs f{};
       fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
       fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
@@ -806,8 +853,8 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
   a.lse_t_in = lse_t;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int ds = (int)qs->size[3], dt = (int)qt->size[3];
-  if (qs->dtype != LARD_DTYPE_F32 && lard::hot_supported(ds, dt, qs->dtype == qt->dtype) &&
-      hot_offsets_ok({qs, ks, qt, kt}, T) && hot_scales_ok(sm_scale_s, sm_scale_t)) {
+  std::string why;
+  if (attn_kl_path(qs, ks, qt, kt, sm_scale_s, sm_scale_t, &why) == LARD_PATH_THROUGHPUT) {
     const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);

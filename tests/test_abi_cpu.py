@@ -292,3 +292,38 @@ def test_counter_summary_scales_by_the_calibration_copy(tmp_path):
     assert out["scale_fetch_bytes_per_count"] == 2048.0 and out["scale_write_bytes_per_count"] == 1024.0
     assert out["read_bytes"]["col_grad"] == 2000 * 2048.0
     assert out["bytes_per_launch"]["col_grad"] == 2000 * 2048.0 + 100 * 1024.0
+
+
+def test_attn_kl_path_names_the_slower_paths_without_a_gpu():
+    """lard_attn_kl_path classifies operands (nothing is launched): the
+    throughput kernels, or the slower path and the condition behind it."""
+    L = _lib.lib()
+
+    def desc(D=128, dtype=1, T=64, H=2, row_stride=None):
+        t = _lib.Tensor4()
+        t.data = 4096
+        t.size[:] = [1, H, T, D]
+        rs = D if row_stride is None else row_stride
+        t.stride[:] = [H * T * rs, T * rs, rs, 1]
+        t.dtype = dtype
+        return t
+
+    def path(qs, qt, ss=0.1, st=0.1):
+        rc = L.lard_attn_kl_path(ctypes.byref(qs), ctypes.byref(qs), ctypes.byref(qt), ctypes.byref(qt), ss, st)
+        return rc, L.lard_last_error().decode()
+
+    assert path(desc(), desc()) == (0, "")
+    rc, why = path(desc(256), desc(256))
+    assert rc == 1 and "head dim 256 > 128" in why
+    rc, why = path(desc(64), desc(128))
+    assert rc == 2 and "64 != teacher head dim 128" in why
+    rc, why = path(desc(dtype=0), desc(dtype=1))
+    assert rc == 2 and "dtypes differ" in why
+    rc, why = path(desc(dtype=2), desc(dtype=2))
+    assert rc == 3 and "float32" in why
+    rc, why = path(desc(), desc(), ss=1e-7)
+    assert rc == 1 and "scales" in why
+    rc, why = path(desc(T=1 << 20, row_stride=2048), desc(T=1 << 20, row_stride=2048))
+    assert rc == 1 and "2^30" in why
+    rc, why = path(desc(D=24), desc(D=24))
+    assert rc == -2 and "supported set" in why  # invalid operands: an error, as for the compute calls

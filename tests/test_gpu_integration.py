@@ -101,6 +101,27 @@ def test_self_relation_fused_and_fallback_dims(gpu_available, dtype, D, T, H):
     assert np.abs(g - rdx).max() / np.abs(rdx).max() <= 2e-2
 
 
+def test_slower_paths_warn_once_per_condition(gpu_available):
+    """Inputs off the throughput kernels (here D = 256, and Ds != Dt) raise one
+    RuntimeWarning per condition naming it; the throughput path warns nothing."""
+    import warnings
+
+    from linearard_amd.attention_KL import attn_kl_align, integration
+
+    integration._WARNED.clear()
+    x = torch.randn((1, 2, 40, 256), device="cuda", dtype=torch.bfloat16)
+    with pytest.warns(RuntimeWarning, match="head dim 256 > 128.*fused-forward"):
+        attn_kl_align(x, x, x, x)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # the same condition again: no second warning
+        attn_kl_align(x, x, x, x)
+        y = torch.randn((1, 2, 40, 128), device="cuda", dtype=torch.bfloat16)
+        attn_kl_align(y, y, y, y)  # throughput kernels: silent
+    z = torch.randn((1, 2, 40, 64), device="cuda", dtype=torch.bfloat16)
+    with pytest.warns(RuntimeWarning, match="student head dim 64 != teacher head dim 128.*stage"):
+        attn_kl_align(z, z, y, y)
+
+
 def test_fused_forward_and_backward_match_stage_kernels(gpu_available):
     """lard_attn_kl_forward / _backward (throughput kernels) against the
     reference-semantics stage kernels: stage A x2, stage B, stage C."""

@@ -52,3 +52,35 @@ def test_stats_table_sorts_by_total_time(tmp_path):
     lines = P.stats_table(str(path)).splitlines()
     assert lines[1].startswith("big") and lines[2].startswith("small")
     assert "4.500" in lines[1] and "90.0%" in lines[1]
+
+
+def test_counter_summary_means_clock_and_mfma_busy(tmp_path):
+    """Two passes, two dispatches of one kernel each, every counter split over
+    two instance rows: the summary sums instances, averages dispatches, takes
+    durations from the timestamps, and derives the clock and MFMA-pipe share."""
+    header = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    name = "void lard::hot_dq_kernel<128, true>(lard::HotArgs)"
+    ms, ghz = 2.0, 2.0
+    cycles = ms * 1e-3 * ghz * 1e9
+
+    def pass_rows(counters, first):
+        rows = []
+        for disp in (first, first + 1):
+            for c, v in counters.items():
+                rows += [[disp, name, c, v / 2, 1000, 1000 + int(ms * 1e6)]] * 2
+        return rows
+
+    p1, p2 = tmp_path / "p1.csv", tmp_path / "p2.csv"
+    _write(p1, header, pass_rows({"GRBM_GUI_ACTIVE": 8 * cycles, "SQ_INSTS_MFMA": 1e6,
+                                  "SQ_VALU_MFMA_BUSY_CYCLES": 0.5 * 1024 * cycles}, 1))
+    _write(p2, header, pass_rows({"GRBM_GUI_ACTIVE": 8 * cycles, "SQ_WAVE_CYCLES": 4e8, "SQ_WAIT_INST_ANY": 1e8}, 9))
+    tab = P.counter_table([str(p1), str(p2)])
+    d = tab["row_grad"]
+    assert d["dispatches"] == 2 and abs(d["duration_ms"] - ms) < 1e-9
+    assert abs(d["clock_ghz"] - ghz) < 1e-9 and d["SQ_INSTS_MFMA"] == 1e6
+    der = P.derived(d)
+    assert abs(der["mfma_busy"] - 0.5) < 1e-9
+    assert abs(der["mfma_cycles_per_inst"] - 0.5 * 1024 * cycles / 1e6) < 1e-6
+    assert abs(der["wave_wait_inst_any"] - 0.25) < 1e-12
+    text = P.counters_report([str(p1), str(p2)])
+    assert "| row_grad |" in text and "mfma_busy" in text and "clock_ghz" in text
