@@ -40,7 +40,6 @@ namespace lard {
 constexpr int kTile = 64;     // rows of K (fwd, dq) or Q (dk) per LDS tile
 constexpr int kWaves = 8;     // waves per workgroup: 8 x 32 rows / columns
 constexpr int kRows = kWaves * 32;
-constexpr int kStages = 3;    // LDS ring depth
 constexpr int kXcds = 8;
 
 struct HotArgs {
@@ -64,7 +63,10 @@ struct HotArgs {
 // the builtin it inserts s_waitcnt vmcnt(0) before every LDS read, which
 // serialises the ring.  The kernels order the copies themselves with
 // wait_vmcnt<N>() + a barrier; the "memory" clobber keeps the compiler from
-// moving LDS accesses across the issue point.
+// moving LDS accesses across the issue point.  M0 is written here and listed
+// as clobbered (the compiler notes that it reserves M0): no compiler-generated
+// code in these kernels uses M0 (every M0 write in the kernels' assembly is
+// this statement's), so no value of its own is live across a copy.
 __device__ __forceinline__ void lds_async16(const void* base, unsigned voff, void* lds_chunk0) {
   // readfirstlane is int -> int: both halves go back through unsigned so the
   // low word is zero-extended (a sign-extended low word would corrupt the
