@@ -41,10 +41,11 @@ def _fwd_bwd(xs, xt, a, mask=None):
     return loss.detach(), x.grad
 
 
-def _check_head(xs, xt, b, h, a, loss_h, grad_h, dtype, chunk=1024):
+def _check_head(xs, xt, b, h, a, loss_h, grad_h, dtype, chunk=1024, mask_b=None):
     x_s = xs[b, h].float().cpu().numpy()
     x_t = xt[b, h].float().cpu().numpy()
-    ref_loss, ref_dx, _, _, kl_rows = O.self_relation_chunked(x_s, x_t, True, a, a, chunk=chunk, dtype=dtype)
+    ref_loss, ref_dx, _, _, kl_rows = O.self_relation_chunked(x_s, x_t, True, a, a, mask=mask_b, chunk=chunk,
+                                                              dtype=dtype)
     assert kl_rows.min() >= -1e-6, kl_rows.min()  # KL >= 0 per row
     assert abs(loss_h - ref_loss) <= LOSS_RTOL * abs(ref_loss), (b, h, loss_h, ref_loss)
     got = grad_h.float().cpu().numpy()
@@ -67,7 +68,8 @@ def _relation(xs, xt, a, heads, mask=None, dtype=np.float32):
             assert torch.equal(dh, dx[b:b + 1, h:h + 1]), f"head ({b}, {h}): gradient differs from the full launch"
             total += lh.double().item()
             if (b, h) in heads:
-                _check_head(xs, xt, b, h, a, lh.double().item(), dh[0, 0], dtype)
+                mb = None if mask is None else mask[b].cpu().numpy()
+                _check_head(xs, xt, b, h, a, lh.double().item(), dh[0, 0], dtype, mask_b=mb)
     assert abs(loss.double().item() - total) <= 1e-5 * abs(total), (loss.item(), total)
     return loss
 

@@ -8,7 +8,9 @@ tests/test_gpu_configs.py.)  Here:
 * at n = 131072 (4x cfg4) one head's LSEs match the chunked oracle on the
   first rows and scipy on the last, the batched API reads the head in place
   from a [B, T, H, D] tensor with the same result as the contiguous copy,
-  and identical relations give exactly zero.
+  and identical relations give exactly zero;
+* a real padding mask at n = 16384 (a padded tail and random holes) against
+  the oracle, with exactly zero gradient on the masked tokens.
 """
 
 import math
@@ -100,3 +102,37 @@ def test_long_context_128k_and_the_strided_view(gpu_available):
     z = attn_kl_align(same, same, xt, xt, causal=True, sm_scale_s=a, sm_scale_t=a)
     z.backward()
     assert z.item() == 0.0 and not bool(same.grad.any())
+
+
+def test_padding_mask_at_16k_against_the_oracle(gpu_available):
+    """A real padding mask at cfg5's sequence length (B=2, H=4, n=16384,
+    d=128, bf16, causal): sequence 0 ends in 2500 padded tokens, sequence 1
+    has 10 % random holes (token 0 kept).  Masked rows and columns take the
+    kernels' token-validity paths on every tile; heads (0, 1) and (1, 3)
+    against the chunked float32 oracle (kernel_A.py:91-120 masking,
+    kernel_C.py:252-256 zero rows and columns), the rest by head
+    independence, and masked tokens get exactly zero gradient."""
+    from tests.test_gpu_configs import _relation
+
+    B, H, n, d = 2, 4, 16384, 128
+    a = 1 / math.sqrt(d)
+    xs, xt = _pair(B, H, n, d, seed=16, noise=0.3)
+    rng = np.random.default_rng(16)
+    mask = np.ones((B, n), dtype=np.int32)
+    mask[0, n - 2500:] = 0
+    mask[1] = rng.random(n) > 0.1
+    mask[1, 0] = 1
+    m = torch.tensor(mask, device="cuda")
+    _relation(xs, xt, a, heads={(0, 1), (1, 3)}, mask=m)
+    _, dx = _fwd_bwd_masked(xs, xt, a, m)
+    assert not bool(dx[0, :, n - 2500:].any())
+    assert not bool(dx[1][:, torch.tensor(mask[1] == 0, device="cuda")].any())
+
+
+def _fwd_bwd_masked(xs, xt, a, mask):
+    from linearard_amd.attention_KL import attn_kl_align
+
+    x = xs.detach().clone().requires_grad_(True)
+    loss = attn_kl_align(x, x, xt, xt, attn_mask=mask, causal=True, sm_scale_s=a, sm_scale_t=a)
+    loss.backward()
+    return loss.detach(), x.grad
