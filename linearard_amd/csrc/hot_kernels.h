@@ -1114,6 +1114,9 @@ struct HotBatch {
   int first[kMaxRelations + 1];   // work items before relation r; first[n] = total
   HotArgs rel[kMaxRelations];
 };
+// The batch travels by value as the kernel's argument block, whose size HIP
+// limits to 4 KiB.
+static_assert(sizeof(HotBatch) <= 4096, "HotBatch exceeds the 4 KiB kernel-argument limit");
 
 // work items (workgroups) of one relation: row blocks x B x heads
 __host__ __device__ inline int fwd_items(const HotArgs& f) { return (f.r.T + kRows - 1) / kRows * f.r.B * f.r.Hq; }
