@@ -225,7 +225,16 @@ def cpu_baseline(n, d, relations):
     }
 
 
-KERNELS = ("forward", "row_grad", "col_grad")
+KERNELS = ("forward", "forward_rowgrad", "row_grad", "col_grad")
+# Algorithmic flops credited to each kernel, in units of d P per (b, h): the
+# 12 d P of a fwd+bwd split as the work each kernel owns.  Forward: S_s and
+# S_t (4).  Forward with the row-side gradient: S_s, S_t and the D K product
+# (6; it executes 8, the product as P_s K and P_t K).  Backward row side: half
+# of the S recompute plus D K (4; it executes 6).  Column side: 4 next to the
+# row-side kernel, or the whole S recompute plus D^T Q (6) after the
+# row-gradient forward.
+KERNEL_CREDIT = {"split": {"forward": 4, "row_grad": 4, "col_grad": 4},
+                 "rowgrad": {"forward_rowgrad": 6, "col_grad": 6}}
 
 
 def traffic_summary(config):
@@ -688,10 +697,11 @@ def main():
     ms = elapsed / args.steps * 1e3
     flops = algorithmic_flops(B, H, n, d)
     rows = B * H * n
-    # 4 d P algorithmic flops per (b, h) for each of the three kernels.
-    per_launch = flops / 3
+    scheme = "rowgrad" if "forward_rowgrad" in kernel_ms else "split"
+    credit = KERNEL_CREDIT[scheme]
     dom_name = max(kernel_ms, key=kernel_ms.get)
     dom_ms = kernel_ms[dom_name]
+    per_launch = flops * credit.get(dom_name, 0) / 12
     achieved = per_launch / (dom_ms * 1e-3) / 1e12
     summary = traffic_summary(args.config)
     traffic = None
@@ -728,7 +738,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom_name, "achieved": achieved,
                      "peak": MI355X_BF16_DENSE_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MI355X_BF16_DENSE_TFLOPS, "traffic": traffic,
-                     "flop_per_launch": per_launch, "avg_launch_ms": dom_ms},
+                     "flop_per_launch": per_launch, "avg_launch_ms": dom_ms,
+                     "credit_dP_per_relation": credit},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

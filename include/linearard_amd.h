@@ -201,6 +201,43 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Autograd forward with the row side of the backward -- AttnKLAlignFn.forward
+ * (integration.py:8-45) for a caller that will run the backward: the same
+ * outputs as lard_attn_kl_forward (same workspace) plus
+ *   dq_row_out[B, Hq, T, Ds] = sm_scale_s sum_j (P_s - P_t)_ij k_s[j]
+ * (float32, 16-byte aligned; the row-side product of kernel_C.py:224-239
+ * without dloss), from the same pass over the keys: the output products
+ * P_s K_s and P_t K_s accumulate next to the online softmaxes, with P_s and
+ * P_t rounded separately to the operand type (the reference rounds their
+ * difference, kernel_C.py:233).  lard_attn_kl_backward_colgrad then runs only
+ * the column side.  Throughput shapes only (lard_attn_kl_path ==
+ * LARD_PATH_THROUGHPUT), else LARD_ERR_UNSUPPORTED.  No counterpart in the
+ * reference, which recomputes both relations in the backward.
+ */
+int lard_attn_kl_forward_rowgrad(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+                                 const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
+                                 float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
+                                 float* dq_row_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Autograd backward after lard_attn_kl_forward_rowgrad --
+ * AttnKLAlignFn.backward (integration.py:48-67) with the row side already
+ * formed: runs the column side (kernel_C.py:242-253, D cast to the student
+ * dtype) and the chain rule with dloss (device scalar, NULL for 1).
+ *   self_relation != 0: dk_out = dloss (dq_row + sm_scale_s sum_h D^T Q_s),
+ *                       the whole gradient of the tensor (dk_out may be dq_row);
+ *   otherwise:          dq_row *= dloss in place (it is then dq), and
+ *                       dk_out = dloss sm_scale_s sum_{h in group} D^T Q_s.
+ * Workspace as lard_attn_kl_backward_workspace_bytes.  Throughput shapes
+ * only, else LARD_ERR_UNSUPPORTED.
+ */
+int lard_attn_kl_backward_colgrad(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s,
+                                  const lard_tensor4* qt, const lard_tensor4* kt, const float* lse_t,
+                                  const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
+                                  const float* dloss, int self_relation, float* dq_row, float* dk_out,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * One self relation of a batched relation loss: the student tensor xs is
  * both q and k, the teacher tensor xt likewise -- the call
  * attn_kl_align(x_s, x_s, x_t, x_t) of train.py:380-402.  lse_s / lse_t
@@ -246,6 +283,27 @@ int lard_attn_kl_batched_forward(const lard_relation* rels, int nrel, const lard
 int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
                                   float sm_scale_s, float sm_scale_t, const float* weights, const float* dloss,
                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Batched forward with the row side of the backward: lard_attn_kl_batched_forward
+ * (train.py:369-410) whose relations also receive, in rels[r].dxs, the row
+ * side of their gradient as lard_attn_kl_forward_rowgrad forms it (no
+ * weight, no dloss).  Pair with lard_attn_kl_batched_backward_colgrad.
+ */
+int lard_attn_kl_batched_forward_rowgrad(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                         float sm_scale_s, float sm_scale_t, const float* weights, float* loss_out,
+                                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Batched backward after lard_attn_kl_batched_forward_rowgrad
+ * (integration.py:48-67 of every relation): adds the column side to the row
+ * side in rels[r].dxs and applies the chain rule once,
+ *   rels[r].dxs = dloss * weights[r] * dKL_r / dxs,
+ * the same result as lard_attn_kl_batched_backward.
+ */
+int lard_attn_kl_batched_backward_colgrad(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                          float sm_scale_s, float sm_scale_t, const float* weights,
+                                          const float* dloss, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * RoPE pair producer -- the step before the path: each model's rotary
@@ -313,7 +371,8 @@ int lard_logits_kl_backward(const lard_logits* t_logits, const lard_logits* s_lo
 #define LARD_KERNEL_COL_GRAD 2 /* backward, column side: dk (kernel_C.py:242-253) */
 #define LARD_KERNEL_LOGITS_FORWARD 3 /* logits KL forward pass (lard_logits_kl_forward) */
 #define LARD_KERNEL_LOGITS_GRAD 4    /* logits KL gradient pass (lard_logits_kl_backward) */
-#define LARD_KERNEL_COUNT 5
+#define LARD_KERNEL_FORWARD_ROWGRAD 5 /* forward with the row-side gradient (lard_attn_kl_*forward_rowgrad) */
+#define LARD_KERNEL_COUNT 6
 
 /*
  * Timing hook for measurement harnesses -- no counterpart in the reference

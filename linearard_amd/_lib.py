@@ -98,7 +98,19 @@ SIGNATURES = {
     "lard_attn_kl_backward": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, _FP, ctypes.c_int, _FP, _FP, ctypes.c_void_p,
                                              ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_attn_kl_forward_rowgrad": (ctypes.c_int, [_T4P, _T4P, _T4P, _T4P, _MP, ctypes.c_int, ctypes.c_float,
+                                                    ctypes.c_float, _FP, _FP, _FP, _FP, ctypes.c_void_p,
+                                                    ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_attn_kl_backward_colgrad": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int,
+                                                     ctypes.c_float, ctypes.c_float, _FP, ctypes.c_int, _FP, _FP,
+                                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "lard_attn_kl_batched_workspace_bytes": (ctypes.c_size_t, [_RP, ctypes.c_int]),
+    "lard_attn_kl_batched_forward_rowgrad": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
+                                                            ctypes.c_float, _FP, _FP, ctypes.c_void_p,
+                                                            ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_attn_kl_batched_backward_colgrad": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
+                                                             ctypes.c_float, _FP, _FP, ctypes.c_void_p,
+                                                             ctypes.c_size_t, ctypes.c_void_p]),
     "lard_attn_kl_batched_forward": (ctypes.c_int, [_RP, ctypes.c_int, _MP, ctypes.c_int, ctypes.c_float,
                                                     ctypes.c_float, _FP, _FP, ctypes.c_void_p, ctypes.c_size_t,
                                                     ctypes.c_void_p]),
@@ -117,7 +129,8 @@ SIGNATURES = {
                                         ctypes.POINTER(ctypes.c_int64)]),
 }
 
-KERNEL_IDS = {"forward": 0, "row_grad": 1, "col_grad": 2, "logits_forward": 3, "logits_grad": 4}
+KERNEL_IDS = {"forward": 0, "row_grad": 1, "col_grad": 2, "logits_forward": 3, "logits_grad": 4,
+              "forward_rowgrad": 5}
 
 _LIB = None
 

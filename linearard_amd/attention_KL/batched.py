@@ -11,7 +11,12 @@ divides by the number of layers (train.py:410).  That is 3 L calls and
 ``sum_r weights[r] * attn_kl_align(xs[r], xs[r], xt[r], xt[r])`` with one
 launch per 8 relations (``lard_attn_kl_batched_forward`` / ``_backward``):
 the relations' row blocks share one grid even when their head counts differ
-(Q/Q 32 heads next to K/K 8).  ``relation_kl_loss`` builds the weights of
+(Q/Q 32 heads next to K/K 8).  When the students need gradients the forward
+is ``lard_attn_kl_batched_forward_rowgrad``, which also leaves the row side
+of every gradient in the float32 buffers the backward returns, and the
+backward (``lard_attn_kl_batched_backward_colgrad``) adds the column side in
+place; a second backward through the same graph runs the full
+``lard_attn_kl_batched_backward``.  ``relation_kl_loss`` builds the weights of
 the train.py formula from the layers' tensors.  Batches outside the batched
 kernels (different head dims, D = 256, extreme scales) go relation by
 relation through the single-relation entry points inside the same autograd
@@ -70,16 +75,22 @@ class AttnKLBatchedFn(torch.autograd.Function):
         md = _lib.mask_desc(attn_mask)
         stream = _lib.stream_of(xs[0])
         batched = len(set(ss)) == 1 and len(set(st)) == 1
+        row_grad = None
         if batched:
-            rels = _relations(xs, xt, lse_s, lse_t)
+            want_grad = any(ctx.needs_input_grad[6:6 + n])
+            if want_grad:
+                row_grad = [torch.empty(x.shape, device=dev, dtype=torch.float32) for x in xs]
+            rels = _relations(xs, xt, lse_s, lse_t, row_grad)
             ws_bytes = L.lard_attn_kl_batched_workspace_bytes(rels, n)
             ws = _workspace(ws_bytes, dev)
-            rc = L.lard_attn_kl_batched_forward(rels, n, ctypes.byref(md), int(bool(causal)), ss[0], st[0],
-                                                weights.data_ptr(), loss.data_ptr(), ws.data_ptr(), ws_bytes, stream)
+            fn = L.lard_attn_kl_batched_forward_rowgrad if want_grad else L.lard_attn_kl_batched_forward
+            rc = fn(rels, n, ctypes.byref(md), int(bool(causal)), ss[0], st[0], weights.data_ptr(), loss.data_ptr(),
+                    ws.data_ptr(), ws_bytes, stream)
             if rc == _lib.LARD_ERR_UNSUPPORTED:
                 batched = False
+                row_grad = None
             else:
-                _lib.check(rc, "lard_attn_kl_batched_forward")
+                _lib.check(rc, "lard_attn_kl_batched_forward_rowgrad" if want_grad else "lard_attn_kl_batched_forward")
         if not batched:
             # relation by relation (same kernels as attn_kl_align), summed on the device
             losses = torch.empty((n,), device=dev, dtype=torch.float32)
@@ -96,7 +107,9 @@ class AttnKLBatchedFn(torch.autograd.Function):
             loss = (losses * weights).sum()
 
         saved_mask = attn_mask if attn_mask is not None else torch.empty(0, device=dev)
-        ctx.save_for_backward(weights, saved_mask, *xs, *xt, *lse_s, *lse_t)
+        ctx.has_row_grad = row_grad is not None
+        ctx.row_grad_used = False
+        ctx.save_for_backward(weights, saved_mask, *xs, *xt, *lse_s, *lse_t, *(row_grad or []))
         ctx.n = n
         ctx.has_mask = attn_mask is not None
         ctx.causal = bool(causal)
@@ -117,6 +130,17 @@ class AttnKLBatchedFn(torch.autograd.Function):
         L = _lib.lib()
         md = _lib.mask_desc(attn_mask)
         stream = _lib.stream_of(xs[0])
+        if ctx.has_row_grad and not ctx.row_grad_used:
+            ctx.row_grad_used = True
+            dxs = list(saved[2 + 4 * n:2 + 5 * n])
+            rels = _relations(xs, xt, lse_s, lse_t, dxs)
+            ws_bytes = L.lard_attn_kl_batched_workspace_bytes(rels, n)
+            ws = _workspace(ws_bytes, dev)
+            rc = L.lard_attn_kl_batched_backward_colgrad(rels, n, ctypes.byref(md), int(ctx.causal), ctx.ss[0],
+                                                         ctx.st[0], weights.data_ptr(), dloss.data_ptr(),
+                                                         ws.data_ptr(), ws_bytes, stream)
+            _lib.check(rc, "lard_attn_kl_batched_backward_colgrad")
+            return (None, None, None, None, None, None, *dxs, *([None] * n))
         dxs = [torch.empty(x.shape, device=dev, dtype=torch.float32) for x in xs]
         if ctx.batched:
             rels = _relations(xs, xt, lse_s, lse_t, dxs)

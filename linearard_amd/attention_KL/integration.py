@@ -14,6 +14,15 @@ to the input dtype before the product like kernel_C.py:233.  For the train.py
 call ``attn_kl_align(x, x, y, y)`` (q is k) the library sums dq + dk in place
 and the Function returns that whole gradient of ``x`` once (None for the
 second input) instead of two float32 tensors for autograd to add.
+
+When the student needs a gradient and the operands take the throughput
+kernels, the forward is ``lard_attn_kl_forward_rowgrad`` instead: the same
+pass also forms the row side of the gradient (dq before dloss, a float32
+[B, Hq, T, Ds] buffer kept for the backward, O(n d) like the gradient
+itself), and the backward runs only the column side
+(``lard_attn_kl_backward_colgrad``), which adds itself to that buffer in
+place.  A second backward through the same graph (retain_graph) finds the
+buffer consumed and runs the full ``lard_attn_kl_backward``.
 """
 
 from __future__ import annotations
@@ -73,16 +82,31 @@ class AttnKLAlignFn(torch.autograd.Function):
         ws_bytes = L.lard_attn_kl_forward_workspace_bytes(B, Hq, T)
         ws = _workspace(ws_bytes, dev)
         d = [_lib.tensor4(x) for x in (qs, ks, qt, kt)]
+        path = "throughput"
         if B * Hq * T > 0:
             _warn_slow_path(d, ss, st)
+            path = kernel_path(d, ss, st)[0]
         md = _lib.mask_desc(attn_mask)
-        rc = L.lard_attn_kl_forward(ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), ctypes.byref(d[3]),
-                                    ctypes.byref(md), int(bool(causal)), ss, st, lse_s.data_ptr(), lse_t.data_ptr(),
-                                    loss.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(qs))
-        _lib.check(rc, "lard_attn_kl_forward")
+        dq_row = None
+        if path == "throughput" and B * Hq * T > 0 and (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]):
+            dq_row = torch.empty((B, Hq, T, Ds), device=dev, dtype=torch.float32)
+            rc = L.lard_attn_kl_forward_rowgrad(
+                ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), ctypes.byref(d[3]), ctypes.byref(md),
+                int(bool(causal)), ss, st, lse_s.data_ptr(), lse_t.data_ptr(), loss.data_ptr(), dq_row.data_ptr(),
+                ws.data_ptr(), ws_bytes, _lib.stream_of(qs))
+            _lib.check(rc, "lard_attn_kl_forward_rowgrad")
+        else:
+            rc = L.lard_attn_kl_forward(ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]),
+                                        ctypes.byref(d[3]), ctypes.byref(md), int(bool(causal)), ss, st,
+                                        lse_s.data_ptr(), lse_t.data_ptr(), loss.data_ptr(), ws.data_ptr(), ws_bytes,
+                                        _lib.stream_of(qs))
+            _lib.check(rc, "lard_attn_kl_forward")
 
         saved_mask = attn_mask if attn_mask is not None else torch.empty(0, device=dev)
-        ctx.save_for_backward(qs, ks, lse_s, qt, kt, lse_t, saved_mask)
+        ctx.has_row_grad = dq_row is not None
+        ctx.row_grad_used = False
+        ctx.save_for_backward(qs, ks, lse_s, qt, kt, lse_t, saved_mask,
+                              dq_row if dq_row is not None else torch.empty(0, device=dev))
         ctx.has_mask = attn_mask is not None
         ctx.causal = bool(causal)
         ctx.sm_scale_s = ss
@@ -93,19 +117,33 @@ class AttnKLAlignFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dloss):
         """integration.py:48-67: stage C and the chain rule with dloss."""
-        qs, ks, lse_s, qt, kt, lse_t, saved_mask = ctx.saved_tensors
+        qs, ks, lse_s, qt, kt, lse_t, saved_mask, dq_row = ctx.saved_tensors
         attn_mask = saved_mask if ctx.has_mask else None
         dloss = dloss.detach().to(torch.float32).contiguous()
         B, Hq, T, Ds = qs.shape
         self_rel = ctx.self_relation
         dev = qs.device
-        dk = torch.empty((B, ks.shape[1], T, Ds), device=dev, dtype=torch.float32)
-        dq = None if self_rel else torch.empty((B, Hq, T, Ds), device=dev, dtype=torch.float32)
         L = _lib.lib()
         ws_bytes = L.lard_attn_kl_backward_workspace_bytes(B, Hq, ks.shape[1], T, Ds, int(self_rel))
         ws = _workspace(ws_bytes, dev)
         d = [_lib.tensor4(x) for x in (qs, ks, qt, kt)]
         md = _lib.mask_desc(attn_mask)
+        if ctx.has_row_grad and not ctx.row_grad_used:
+            # the row side came with the forward: the column side adds itself
+            # to it in place (self relation) or dq_row becomes dq
+            ctx.row_grad_used = True
+            dk = dq_row if self_rel else torch.empty((B, ks.shape[1], T, Ds), device=dev, dtype=torch.float32)
+            rc = L.lard_attn_kl_backward_colgrad(
+                ctypes.byref(d[0]), ctypes.byref(d[1]), lse_s.data_ptr(), ctypes.byref(d[2]), ctypes.byref(d[3]),
+                lse_t.data_ptr(), ctypes.byref(md), int(ctx.causal), ctx.sm_scale_s, ctx.sm_scale_t,
+                dloss.data_ptr(), int(self_rel), dq_row.data_ptr(), dk.data_ptr(), ws.data_ptr(), ws_bytes,
+                _lib.stream_of(qs))
+            _lib.check(rc, "lard_attn_kl_backward_colgrad")
+            if self_rel:
+                return dk, None, None, None, None, None, None, None
+            return dq_row, dk, None, None, None, None, None, None
+        dk = torch.empty((B, ks.shape[1], T, Ds), device=dev, dtype=torch.float32)
+        dq = None if self_rel else torch.empty((B, Hq, T, Ds), device=dev, dtype=torch.float32)
         rc = L.lard_attn_kl_backward(
             ctypes.byref(d[0]), ctypes.byref(d[1]), lse_s.data_ptr(), ctypes.byref(d[2]), ctypes.byref(d[3]),
             lse_t.data_ptr(), ctypes.byref(md), int(ctx.causal), ctx.sm_scale_s, ctx.sm_scale_t, dloss.data_ptr(),

@@ -17,7 +17,7 @@
 #include <string>
 
 #include "../../include/linearard_amd.h"
-#include "hot_kernels.h"
+#include "hot_fwdq.h"
 #include "logits_kl_kernels.h"
 #include "rope_kernels.h"
 #include "stage_f32.h"
@@ -913,6 +913,117 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                     "attn_kl_backward dk launch");
 }
 
+int lard_attn_kl_forward_rowgrad(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
+                                 const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
+                                 float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
+                                 float* dq_row_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
+  if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
+  if (qs->size[0] != qt->size[0] || qs->size[1] != qt->size[1] || qs->size[2] != qt->size[2])
+    return fail(LARD_ERR_INVALID_ARGUMENT, "student/teacher B/Hq/T must align");
+  if ((rc = check_mask(mask, qs->size[0], qs->size[2])) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_s, "sm_scale_s")) != LARD_OK) return rc;
+  if ((rc = check_scale(sm_scale_t, "sm_scale_t")) != LARD_OK) return rc;
+  if (loss_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "loss_out must not be NULL");
+  std::string why;
+  if (attn_kl_path(qs, ks, qt, kt, sm_scale_s, sm_scale_t, &why) != LARD_PATH_THROUGHPUT)
+    return fail(LARD_ERR_UNSUPPORTED, "the row-gradient forward runs on the throughput kernels only (%s)",
+                why.c_str());
+  const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
+  const int64_t n = B * Hq * T;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n == 0)
+    return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "attn_kl_forward reduce launch");
+  if (lse_s_out == nullptr || lse_t_out == nullptr || dq_row_out == nullptr)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "lse and dq_row outputs must not be NULL");
+  if (reinterpret_cast<uintptr_t>(dq_row_out) % 16 != 0)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "dq_row_out must be 16-byte aligned");
+  if ((rc = check_grid(B * Hq)) != LARD_OK) return rc;
+  if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
+  const size_t need = lard_attn_kl_forward_workspace_bytes(B, Hq, T);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
+  lard::HotArgs f{};
+  fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
+  fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
+  fill_common(f.r, B, Hq, T, mask, causal);
+  f.lse_s_out = lse_s_out;
+  f.lse_t_out = lse_t_out;
+  f.row_out = w.loss.rows;
+  f.dq_out = dq_row_out;
+  f.Tp = (int)padded_len(T);
+  f.tok_ok = w.tok_ok;
+  f.first2 = w.first2;
+  if ((rc = hip_status(lard::launch_token_prep(f.r, f.Tp, w.tok_ok, w.first2, st),
+                       "attn_kl_forward_rowgrad token prep launch")) != LARD_OK)
+    return rc;
+  const bool bf = qs->dtype == LARD_DTYPE_BF16;
+  if ((rc = hip_status(timed(LARD_KERNEL_FORWARD_ROWGRAD, st,
+                             [&] { return lard::launch_hot_fwdq(f, padded_dim(qs->size[3]), bf, st); }),
+                       "attn_kl_forward_rowgrad launch")) != LARD_OK)
+    return rc;
+  return hip_status(lard::launch_reduce_sum(w.loss.rows, n, w.loss.partial, loss_out, st),
+                    "attn_kl_forward_rowgrad reduce launch");
+}
+
+int lard_attn_kl_backward_colgrad(const lard_tensor4* qs, const lard_tensor4* ks, const float* lse_s,
+                                  const lard_tensor4* qt, const lard_tensor4* kt, const float* lse_t,
+                                  const lard_mask* mask, int causal, float sm_scale_s, float sm_scale_t,
+                                  const float* dloss, int self_relation, float* dq_row, float* dk_out,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_two_sided(qs, ks, lse_s, qt, kt, lse_t, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  const int64_t B = qs->size[0], Hq = qs->size[1], T = qs->size[2];
+  if (B * Hq * T == 0) return ok();
+  if (dk_out == nullptr || dq_row == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "dq_row and dk_out must not be NULL");
+  if (self_relation) {
+    if (ks->size[1] != Hq || qs->data != ks->data || qs->stride[0] != ks->stride[0] ||
+        qs->stride[1] != ks->stride[1] || qs->stride[2] != ks->stride[2])
+      return fail(LARD_ERR_INVALID_ARGUMENT, "self relation needs q and k to be the same tensor");
+  }
+  std::string why;
+  if (attn_kl_path(qs, ks, qt, kt, sm_scale_s, sm_scale_t, &why) != LARD_PATH_THROUGHPUT)
+    return fail(LARD_ERR_UNSUPPORTED, "the column-gradient backward runs on the throughput kernels only (%s)",
+                why.c_str());
+  const int ds = (int)qs->size[3];
+  const size_t need = lard_attn_kl_backward_workspace_bytes(B, Hq, ks->size[1], T, ds, self_relation);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Tp = (int)padded_len(T);
+  const BwdWs w = bwd_layout(workspace, B, Hq, T, nullptr);
+  lard::HotArgs f{};
+  fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
+  fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
+  fill_common(f.r, B, Hq, T, mask, causal);
+  f.r.lse_s_in = lse_s;
+  f.r.lse_t_in = lse_t;
+  if ((rc = hip_status(lard::launch_token_prep(f.r, Tp, w.tok_ok, w.first2, st),
+                       "attn_kl_backward_colgrad token prep launch")) != LARD_OK)
+    return rc;
+  if ((rc = hip_status(lard::launch_row_prep(f.r, Tp, w.tok_ok, w.first2, w.nl_s, w.nl_t, st),
+                       "attn_kl_backward_colgrad row prep launch")) != LARD_OK)
+    return rc;
+  f.Tp = Tp;
+  f.tok_ok = w.tok_ok;
+  f.first2 = w.first2;
+  f.nl_s = w.nl_s;
+  f.nl_t = w.nl_t;
+  f.r.dk_out = dk_out;
+  f.r.dk_add = self_relation ? dq_row : nullptr;
+  f.r.dscale = dloss;
+  const bool bf = qs->dtype == LARD_DTYPE_BF16;
+  if ((rc = hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_hot_bwd(f, padded_dim(ds), bf, st); }),
+                       "attn_kl_backward_colgrad dk launch")) != LARD_OK)
+    return rc;
+  if (self_relation) return ok();
+  return hip_status(lard::launch_scale_inplace(dq_row, B * Hq * T * qs->size[3], dloss, st),
+                    "attn_kl_backward_colgrad dq scale launch");
+}
+
 size_t lard_attn_kl_batched_workspace_bytes(const lard_relation* rels, int nrel) {
   if (rels == nullptr || nrel < 1) return 0;
   size_t bytes = 0;
@@ -1032,6 +1143,121 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
       return rc;
     if ((rc = hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_hot_bwd_batch(mk, dp, bf, st); }),
                          "batched backward dk launch")) != LARD_OK)
+      return rc;
+  }
+  return ok();
+}
+
+int lard_attn_kl_batched_forward_rowgrad(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                         float sm_scale_s, float sm_scale_t, const float* weights, float* loss_out,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_batch(rels, nrel, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  if (loss_out == nullptr) return fail(LARD_ERR_INVALID_ARGUMENT, "loss_out must not be NULL");
+  int64_t rows = 0;
+  for (int r = 0; r < nrel; ++r) {
+    if (rel_rows(rels[r]) > 0 && (rels[r].lse_s == nullptr || rels[r].lse_t == nullptr || rels[r].dxs == nullptr))
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: lse outputs and dxs must not be NULL", r);
+    if (rels[r].dxs != nullptr && reinterpret_cast<uintptr_t>(rels[r].dxs) % 16 != 0)
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: dxs must be 16-byte aligned", r);
+    rows += rel_rows(rels[r]);
+  }
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0)
+    return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "batched forward reduce launch");
+  const size_t need = lard_attn_kl_batched_workspace_bytes(rels, nrel);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  const BatchWs w = batch_layout(workspace, rels, nrel, nullptr);
+  const int Tp = (int)padded_len(rels[0].xs.size[2]);
+  const int dp = padded_dim(rels[0].xs.size[3]);
+  const bool bf = rels[0].xs.dtype == LARD_DTYPE_BF16;
+  {
+    const lard::HotArgs f0 = relation_args(rels[0], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok, w.first2);
+    if ((rc = hip_status(lard::launch_token_prep(f0.r, Tp, w.tok_ok, w.first2, st),
+                         "batched forward_rowgrad token prep launch")) != LARD_OK)
+      return rc;
+  }
+  int64_t row_off = 0;
+  for (int g = 0; g < nrel; g += lard::kMaxRelations) {
+    lard::HotBatch m{};
+    for (int r = g; r < nrel && r < g + lard::kMaxRelations; ++r) {
+      if (rel_rows(rels[r]) == 0) continue;
+      lard::HotArgs f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok, w.first2);
+      f.lse_s_out = rels[r].lse_s;
+      f.lse_t_out = rels[r].lse_t;
+      f.row_out = w.loss.rows + row_off;
+      f.dq_out = rels[r].dxs;
+      f.r.weight = weights != nullptr ? weights + r : nullptr;
+      row_off += rel_rows(rels[r]);
+      m.rel[m.n++] = f;
+    }
+    if (m.n == 0) continue;
+    if ((rc = hip_status(timed(LARD_KERNEL_FORWARD_ROWGRAD, st,
+                               [&] { return lard::launch_hot_fwdq_batch(m, dp, bf, st); }),
+                         "batched forward_rowgrad launch")) != LARD_OK)
+      return rc;
+  }
+  return hip_status(lard::launch_reduce_sum(w.loss.rows, rows, w.loss.partial, loss_out, st),
+                    "batched forward_rowgrad reduce launch");
+}
+
+int lard_attn_kl_batched_backward_colgrad(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
+                                          float sm_scale_s, float sm_scale_t, const float* weights,
+                                          const float* dloss, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_batch(rels, nrel, mask, sm_scale_s, sm_scale_t)) != LARD_OK) return rc;
+  int64_t rows = 0;
+  for (int r = 0; r < nrel; ++r) {
+    if (rel_rows(rels[r]) > 0 && (rels[r].lse_s == nullptr || rels[r].lse_t == nullptr || rels[r].dxs == nullptr))
+      return fail(LARD_ERR_INVALID_ARGUMENT, "relation %d: lse inputs and dxs must not be NULL", r);
+    rows += rel_rows(rels[r]);
+  }
+  if (rows == 0) return ok();
+  const size_t need = lard_attn_kl_batched_workspace_bytes(rels, nrel);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const BatchWs w = batch_layout(workspace, rels, nrel, nullptr);
+  const int Tp = (int)padded_len(rels[0].xs.size[2]);
+  const int dp = padded_dim(rels[0].xs.size[3]);
+  const bool bf = rels[0].xs.dtype == LARD_DTYPE_BF16;
+  std::vector<lard::HotArgs> fs((size_t)nrel);
+  int64_t nl_off = 0;
+  for (int r = 0; r < nrel; ++r) {
+    lard::HotArgs& f = fs[(size_t)r];
+    f = relation_args(rels[r], mask, causal, sm_scale_s, sm_scale_t, Tp, w.tok_ok, w.first2);
+    f.r.lse_s_in = rels[r].lse_s;
+    f.r.lse_t_in = rels[r].lse_t;
+    float* nl_s = w.nl_s + nl_off;
+    float* nl_t = w.nl_t + nl_off;
+    f.nl_s = nl_s;
+    f.nl_t = nl_t;
+    nl_off += rels[r].xs.size[0] * rels[r].xs.size[1] * (int64_t)Tp;
+    if (r == 0 && (rc = hip_status(lard::launch_token_prep(f.r, Tp, w.tok_ok, w.first2, st),
+                                   "batched backward_colgrad token prep launch")) != LARD_OK)
+      return rc;
+    if (rel_rows(rels[r]) > 0 &&
+        (rc = hip_status(lard::launch_row_prep(f.r, Tp, w.tok_ok, w.first2, nl_s, nl_t, st),
+                         "batched backward_colgrad row prep launch")) != LARD_OK)
+      return rc;
+  }
+  for (int g = 0; g < nrel; g += lard::kMaxRelations) {
+    // the column side adds itself to the row side in place and applies
+    // dloss * weight once
+    lard::HotBatch mk{};
+    for (int r = g; r < nrel && r < g + lard::kMaxRelations; ++r) {
+      if (rel_rows(rels[r]) == 0) continue;
+      lard::HotArgs f = fs[(size_t)r];
+      f.r.dk_out = rels[r].dxs;
+      f.r.dk_add = rels[r].dxs;
+      f.r.dscale = dloss;
+      f.r.weight = weights != nullptr ? weights + r : nullptr;
+      mk.rel[mk.n++] = f;
+    }
+    if (mk.n == 0) continue;
+    if ((rc = hip_status(timed(LARD_KERNEL_COL_GRAD, st, [&] { return lard::launch_hot_bwd_batch(mk, dp, bf, st); }),
+                         "batched backward_colgrad dk launch")) != LARD_OK)
       return rc;
   }
   return ok();

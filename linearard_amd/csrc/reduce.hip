@@ -54,4 +54,21 @@ hipError_t launch_reduce_sum(const float* x, int64_t n, double* partial, float* 
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(kReduceThreads) void scale_inplace_kernel(float* __restrict__ x, int64_t n4,
+                                                                        const float* __restrict__ dscale) {
+  const float s = *dscale;
+  f32x4* v = reinterpret_cast<f32x4*>(x);
+  for (int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kReduceThreads)
+    v[i] *= s;
+}
+
+hipError_t launch_scale_inplace(float* x, int64_t n, const float* dscale, hipStream_t stream) {
+  if (n <= 0 || dscale == nullptr) return hipSuccess;
+  const int64_t n4 = n / 4;
+  const int64_t want = (n4 + kReduceThreads - 1) / kReduceThreads;
+  const int blocks = (int)(want < 4096 ? want : 4096);
+  hipLaunchKernelGGL(scale_inplace_kernel, dim3(blocks), dim3(kReduceThreads), 0, stream, x, n4, dscale);
+  return hipGetLastError();
+}
+
 }  // namespace lard

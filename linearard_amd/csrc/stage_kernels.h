@@ -418,5 +418,8 @@ hipError_t launch_col_dk(const RelArgs& a, int dps, int dpt, hipStream_t stream)
 // Loss reduction: out = sum(x[0..n)) through kReduceBlocks double partials.
 constexpr int kReduceBlocks = 512;
 hipError_t launch_reduce_sum(const float* x, int64_t n, double* partial, float* out, hipStream_t stream);
+// x[0..n) *= (*dscale) in place (dscale a device scalar; n a multiple of 4,
+// x 16-byte aligned): the chain rule of a gradient computed before dloss.
+hipError_t launch_scale_inplace(float* x, int64_t n, const float* dscale, hipStream_t stream);
 
 }  // namespace lard

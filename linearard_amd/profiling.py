@@ -33,6 +33,8 @@ import sys
 
 # kernel-name fragment -> timing-hook kernel id (include/linearard_amd.h)
 KERNEL_NAMES = {
+    "hot_fwdq_kernel": "forward_rowgrad",
+    "hot_fwdq_batch_kernel": "forward_rowgrad",
     "hot_fwd_kernel": "forward",
     "fused_fwd_kernel": "forward",
     "hot_dq_kernel": "row_grad",
@@ -107,7 +109,7 @@ def traffic(fetch_csv: str, write_csv: str, calib_mib: int, config: str) -> dict
 
 # MI355X: 8 XCDs, 32 CUs per XCD, 4 SIMDs per CU, 4 shader engines per XCD.
 XCDS, CUS, SIMDS, SES = 8, 256, 1024, 32
-KERNEL_ORDER = ("forward", "row_grad", "col_grad", "logits_forward", "logits_grad")
+KERNEL_ORDER = ("forward", "forward_rowgrad", "row_grad", "col_grad", "logits_forward", "logits_grad")
 
 
 def counter_table(paths) -> dict:
