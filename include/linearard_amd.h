@@ -208,12 +208,23 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
  * (float32, 16-byte aligned; the row-side product of kernel_C.py:224-239
  * without dloss), from the same pass over the keys: the output products
  * P_s K_s and P_t K_s accumulate next to the online softmaxes, with P_s and
- * P_t rounded separately to the operand type (the reference rounds their
- * difference, kernel_C.py:233).  lard_attn_kl_backward_colgrad then runs only
+ * P_t rounded separately to float16 (the reference rounds their difference
+ * to the input type, kernel_C.py:233) and both relations' scores from
+ * float16 operands (bfloat16 inputs are converted into the workspace, each
+ * side scaled by a power of two when it holds values of 2^15 or more; the
+ * products are those of the input values).  Workspace:
+ * lard_attn_kl_forward_rowgrad_workspace_bytes.  lard_attn_kl_backward_colgrad then runs only
  * the column side.  Throughput shapes only (lard_attn_kl_path ==
  * LARD_PATH_THROUGHPUT), else LARD_ERR_UNSUPPORTED.  No counterpart in the
  * reference, which recomputes both relations in the backward.
  */
+/* Workspace needed by lard_attn_kl_forward_rowgrad (bytes): the forward's,
+ * plus both sides' keys as float16 ([B, kv_heads, T, D] student,
+ * [B, kv_heads_t, T, D] teacher; bfloat16 inputs are converted) and four
+ * scalars. */
+size_t lard_attn_kl_forward_rowgrad_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                                    int64_t kv_heads_t, int64_t seq_len, int64_t head_dim);
+
 int lard_attn_kl_forward_rowgrad(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
                                  const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
                                  float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
@@ -288,8 +299,14 @@ int lard_attn_kl_batched_backward(const lard_relation* rels, int nrel, const lar
  * Batched forward with the row side of the backward: lard_attn_kl_batched_forward
  * (train.py:369-410) whose relations also receive, in rels[r].dxs, the row
  * side of their gradient as lard_attn_kl_forward_rowgrad forms it (no
- * weight, no dloss).  Pair with lard_attn_kl_batched_backward_colgrad.
+ * weight, no dloss).  Workspace: lard_attn_kl_batched_rowgrad_workspace_bytes.
+ * Pair with lard_attn_kl_batched_backward_colgrad (which takes the smaller
+ * lard_attn_kl_batched_workspace_bytes).
  */
+/* Workspace of lard_attn_kl_batched_forward_rowgrad (bytes): the batched
+ * workspace plus each relation's keys (both sides) as float16. */
+size_t lard_attn_kl_batched_rowgrad_workspace_bytes(const lard_relation* rels, int nrel);
+
 int lard_attn_kl_batched_forward_rowgrad(const lard_relation* rels, int nrel, const lard_mask* mask, int causal,
                                          float sm_scale_s, float sm_scale_t, const float* weights, float* loss_out,
                                          void* workspace, size_t workspace_bytes, void* stream);

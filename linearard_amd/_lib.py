@@ -98,6 +98,8 @@ SIGNATURES = {
     "lard_attn_kl_backward": (ctypes.c_int, [_T4P, _T4P, _FP, _T4P, _T4P, _FP, _MP, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, _FP, ctypes.c_int, _FP, _FP, ctypes.c_void_p,
                                              ctypes.c_size_t, ctypes.c_void_p]),
+    "lard_attn_kl_forward_rowgrad_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 6),
+    "lard_attn_kl_batched_rowgrad_workspace_bytes": (ctypes.c_size_t, [_RP, ctypes.c_int]),
     "lard_attn_kl_forward_rowgrad": (ctypes.c_int, [_T4P, _T4P, _T4P, _T4P, _MP, ctypes.c_int, ctypes.c_float,
                                                     ctypes.c_float, _FP, _FP, _FP, _FP, ctypes.c_void_p,
                                                     ctypes.c_size_t, ctypes.c_void_p]),

@@ -81,7 +81,8 @@ class AttnKLBatchedFn(torch.autograd.Function):
             if want_grad:
                 row_grad = [torch.empty(x.shape, device=dev, dtype=torch.float32) for x in xs]
             rels = _relations(xs, xt, lse_s, lse_t, row_grad)
-            ws_bytes = L.lard_attn_kl_batched_workspace_bytes(rels, n)
+            ws_bytes = (L.lard_attn_kl_batched_rowgrad_workspace_bytes(rels, n) if want_grad
+                        else L.lard_attn_kl_batched_workspace_bytes(rels, n))
             ws = _workspace(ws_bytes, dev)
             fn = L.lard_attn_kl_batched_forward_rowgrad if want_grad else L.lard_attn_kl_batched_forward
             rc = fn(rels, n, ctypes.byref(md), int(bool(causal)), ss[0], st[0], weights.data_ptr(), loss.data_ptr(),

@@ -90,6 +90,8 @@ class AttnKLAlignFn(torch.autograd.Function):
         dq_row = None
         if path == "throughput" and B * Hq * T > 0 and (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]):
             dq_row = torch.empty((B, Hq, T, Ds), device=dev, dtype=torch.float32)
+            ws_bytes = L.lard_attn_kl_forward_rowgrad_workspace_bytes(B, Hq, ks.shape[1], kt.shape[1], T, Ds)
+            ws = _workspace(ws_bytes, dev)
             rc = L.lard_attn_kl_forward_rowgrad(
                 ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), ctypes.byref(d[3]), ctypes.byref(md),
                 int(bool(causal)), ss, st, lse_s.data_ptr(), lse_t.data_ptr(), loss.data_ptr(), dq_row.data_ptr(),

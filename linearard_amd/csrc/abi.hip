@@ -278,6 +278,73 @@ FwdWs fwd_layout(void* base, int64_t B, int64_t H, int64_t T, size_t* bytes) {
   return w;
 }
 
+// Forward with the row-side gradient: the forward's regions, then both
+// sides' keys as float16 ([B, Hkv_s, T, D] and [B, Hkv_t, T, D]; bfloat16
+// inputs), the scratch of their maxima and the powers of two they were
+// scaled by.
+struct KeysF16 {
+  lard::u16* k16;
+  unsigned* maxbits;
+  float* scale;
+};
+
+KeysF16 take_keys(Carver& c, int64_t B, int64_t Hkv, int64_t T, int64_t D) {
+  KeysF16 k;
+  k.k16 = c.take<lard::u16>(B * Hkv * T * D);
+  k.maxbits = c.take<unsigned>(1);
+  k.scale = c.take<float>(1);
+  return k;
+}
+
+struct RowgradWs {
+  FwdWs fwd;
+  KeysF16 s, t;
+};
+
+RowgradWs rowgrad_layout(void* base, int64_t B, int64_t Hq, int64_t Hkv_s, int64_t Hkv_t, int64_t T, int64_t D,
+                         size_t* bytes) {
+  size_t fwd_bytes = 0;
+  RowgradWs w;
+  w.fwd = fwd_layout(base, B, Hq, T, &fwd_bytes);
+  Carver c(base != nullptr ? static_cast<char*>(base) + fwd_bytes : nullptr);
+  w.s = take_keys(c, B, Hkv_s, T, D);
+  w.t = take_keys(c, B, Hkv_t, T, D);
+  if (bytes != nullptr) *bytes = fwd_bytes + c.bytes();
+  return w;
+}
+
+// Both sides' float16 keys for the fused row-gradient forward: scaled copies
+// for bfloat16 inputs, the tensors themselves for float16 ones.
+hipError_t keys_f16(lard::HotArgs& f, bool bf, const KeysF16& ks, const KeysF16& kt, hipStream_t st) {
+  if (!bf) {
+    f.k16 = f.r.s.k;
+    f.k16_sb = f.r.s.k_sb;
+    f.k16_sh = f.r.s.k_sh;
+    f.k16_st = f.r.s.k_st;
+    f.k16_scale = nullptr;
+    f.k16t = f.r.t.k;
+    f.k16t_sb = f.r.t.k_sb;
+    f.k16t_sh = f.r.t.k_sh;
+    f.k16t_st = f.r.t.k_st;
+    f.k16t_scale = nullptr;
+    return hipSuccess;
+  }
+  const int64_t D = f.r.s.dim, T = f.r.T;
+  f.k16 = ks.k16;
+  f.k16_st = D;
+  f.k16_sh = T * D;
+  f.k16_sb = (int64_t)f.r.s.hkv * T * D;
+  f.k16_scale = ks.scale;
+  f.k16t = kt.k16;
+  f.k16t_st = D;
+  f.k16t_sh = T * D;
+  f.k16t_sb = (int64_t)f.r.t.hkv * T * D;
+  f.k16t_scale = kt.scale;
+  hipError_t e = lard::launch_keys_f16(f.r.s, f.r.B, f.r.Hq, f.r.T, ks.maxbits, ks.scale, ks.k16, st);
+  if (e != hipSuccess) return e;
+  return lard::launch_keys_f16(f.r.t, f.r.B, f.r.Hq, f.r.T, kt.maxbits, kt.scale, kt.k16, st);
+}
+
 // Backward of the autograd path: token validity, the first two valid tokens
 // of each sequence and the log2-domain row normalisers (the size depends on
 // B, Hq and T only).
@@ -913,6 +980,14 @@ int lard_attn_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const 
                     "attn_kl_backward dk launch");
 }
 
+size_t lard_attn_kl_forward_rowgrad_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                                    int64_t kv_heads_t, int64_t seq_len, int64_t head_dim) {
+  if (batch <= 0 || heads <= 0 || kv_heads <= 0 || kv_heads_t <= 0 || seq_len <= 0 || head_dim <= 0) return 0;
+  size_t bytes = 0;
+  rowgrad_layout(nullptr, batch, heads, kv_heads, kv_heads_t, seq_len, head_dim, &bytes);
+  return bytes;
+}
+
 int lard_attn_kl_forward_rowgrad(const lard_tensor4* qs, const lard_tensor4* ks, const lard_tensor4* qt,
                                  const lard_tensor4* kt, const lard_mask* mask, int causal, float sm_scale_s,
                                  float sm_scale_t, float* lse_s_out, float* lse_t_out, float* loss_out,
@@ -941,10 +1016,12 @@ int lard_attn_kl_forward_rowgrad(const lard_tensor4* qs, const lard_tensor4* ks,
     return fail(LARD_ERR_INVALID_ARGUMENT, "dq_row_out must be 16-byte aligned");
   if ((rc = check_grid(B * Hq)) != LARD_OK) return rc;
   if ((rc = check_blocks(B, Hq, T)) != LARD_OK) return rc;
-  const size_t need = lard_attn_kl_forward_workspace_bytes(B, Hq, T);
+  const int64_t Hkv = ks->size[1], Hkv_t = kt->size[1], D = qs->size[3];
+  const size_t need = lard_attn_kl_forward_rowgrad_workspace_bytes(B, Hq, Hkv, Hkv_t, T, D);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
-  const FwdWs w = fwd_layout(workspace, B, Hq, T, nullptr);
+  const RowgradWs rw = rowgrad_layout(workspace, B, Hq, Hkv, Hkv_t, T, D, nullptr);
+  const FwdWs& w = rw.fwd;
   lard::HotArgs f{};
   fill_side(f.r.s, qs, ks, Hq, sm_scale_s);
   fill_side(f.r.t, qt, kt, Hq, sm_scale_t);
@@ -960,6 +1037,9 @@ int lard_attn_kl_forward_rowgrad(const lard_tensor4* qs, const lard_tensor4* ks,
                        "attn_kl_forward_rowgrad token prep launch")) != LARD_OK)
     return rc;
   const bool bf = qs->dtype == LARD_DTYPE_BF16;
+  if ((rc = hip_status(keys_f16(f, bf, rw.s, rw.t, st),
+                       "attn_kl_forward_rowgrad float16 keys launch")) != LARD_OK)
+    return rc;
   if ((rc = hip_status(timed(LARD_KERNEL_FORWARD_ROWGRAD, st,
                              [&] { return lard::launch_hot_fwdq(f, padded_dim(qs->size[3]), bf, st); }),
                        "attn_kl_forward_rowgrad launch")) != LARD_OK)
@@ -1028,6 +1108,41 @@ size_t lard_attn_kl_batched_workspace_bytes(const lard_relation* rels, int nrel)
   if (rels == nullptr || nrel < 1) return 0;
   size_t bytes = 0;
   batch_layout(nullptr, rels, nrel, &bytes);
+  return bytes;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The batched workspace, then per relation both sides' float16 keys.
+struct BatchRowgradWs {
+  BatchWs batch;
+  std::vector<KeysF16> s, t;
+};
+
+BatchRowgradWs batch_rowgrad_layout(void* base, const lard_relation* rels, int nrel, size_t* bytes) {
+  size_t batch_bytes = 0;
+  BatchRowgradWs w;
+  w.batch = batch_layout(base, rels, nrel, &batch_bytes);
+  Carver c(base != nullptr ? static_cast<char*>(base) + batch_bytes : nullptr);
+  for (int r = 0; r < nrel; ++r) {
+    const lard_tensor4& x = rels[r].xs;
+    w.s.push_back(take_keys(c, x.size[0], x.size[1], x.size[2], x.size[3]));
+    w.t.push_back(take_keys(c, x.size[0], x.size[1], x.size[2], x.size[3]));
+  }
+  if (bytes != nullptr) *bytes = batch_bytes + c.bytes();
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t lard_attn_kl_batched_rowgrad_workspace_bytes(const lard_relation* rels, int nrel) {
+  if (rels == nullptr || nrel < 1) return 0;
+  size_t bytes = 0;
+  batch_rowgrad_layout(nullptr, rels, nrel, &bytes);
   return bytes;
 }
 
@@ -1165,10 +1280,11 @@ int lard_attn_kl_batched_forward_rowgrad(const lard_relation* rels, int nrel, co
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (rows == 0)
     return hip_status(lard::launch_reduce_sum(nullptr, 0, nullptr, loss_out, st), "batched forward reduce launch");
-  const size_t need = lard_attn_kl_batched_workspace_bytes(rels, nrel);
+  const size_t need = lard_attn_kl_batched_rowgrad_workspace_bytes(rels, nrel);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(LARD_ERR_INVALID_ARGUMENT, "workspace too small: need %zu bytes", need);
-  const BatchWs w = batch_layout(workspace, rels, nrel, nullptr);
+  const BatchRowgradWs rw = batch_rowgrad_layout(workspace, rels, nrel, nullptr);
+  const BatchWs& w = rw.batch;
   const int Tp = (int)padded_len(rels[0].xs.size[2]);
   const int dp = padded_dim(rels[0].xs.size[3]);
   const bool bf = rels[0].xs.dtype == LARD_DTYPE_BF16;
@@ -1189,6 +1305,9 @@ int lard_attn_kl_batched_forward_rowgrad(const lard_relation* rels, int nrel, co
       f.row_out = w.loss.rows + row_off;
       f.dq_out = rels[r].dxs;
       f.r.weight = weights != nullptr ? weights + r : nullptr;
+      if ((rc = hip_status(keys_f16(f, bf, rw.s[(size_t)r], rw.t[(size_t)r], st),
+                           "batched forward_rowgrad float16 keys launch")) != LARD_OK)
+        return rc;
       row_off += rel_rows(rels[r]);
       m.rel[m.n++] = f;
     }

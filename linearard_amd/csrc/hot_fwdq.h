@@ -16,11 +16,18 @@
 // relation instead of 16 (forward 8, column side 6), and 4 exponentials per
 // element instead of 6.
 //
-// Precision: P_s and P_t enter the products rounded separately to the
-// operand type (the reference rounds their difference D, kernel_C.py:233).
-// The error is then relative to P rather than to D; the kernel's callers
-// choose float16 operands for that reason where the student is float16 (see
-// the parity tests for the measured errors).
+// Precision: P_s and P_t enter the products rounded separately (the
+// reference rounds their difference D to the input type, kernel_C.py:233),
+// so the error is relative to P rather than to D.  The kernel therefore
+// runs in float16 whatever the input type: the output products with
+// float16 probabilities (11 significant bits against bfloat16's 8, so 2^-12
+// relative instead of 2^-9; the lazy maxima keep every probability below
+// 2^15, inside float16's range), and both relations' scores from the same
+// products as in the input type (a bfloat16 value is a float16 value,
+// scaled by a power of two when its tensor holds values of 2^15 or more).
+// Both sides go through the same conversion, so identical relations still
+// give bitwise identical scores (the float16 and bfloat16 MFMAs need not
+// round their sums alike).
 //
 // Layout: one wave per SIMD (4 waves x 32 query rows per workgroup), since
 // the two output accumulators (2 x 4 x 16 float32 per lane at D = 128) do not
@@ -263,14 +270,39 @@ __device__ __forceinline__ void sub_scores_q(const u16* ks, int r0, int l32, int
     const u16* p = row_chunk<DP>(ks, r0 + l32, 2 * kk + half);
     const u16x8 os = *reinterpret_cast<const u16x8*>(p), ot = *reinterpret_cast<const u16x8*>(p + kTile * DP);
     if (kk == 0) {
-      mfma_first<BF>(ss, os, fq_s[0]);
-      mfma_first<BF>(st, ot, fq_t[0]);
+      mfma_first<false>(ss, os, fq_s[0]);
+      mfma_first<false>(st, ot, fq_t[0]);
     } else {
-      mfma_next<BF>(ss, os, fq_s[kk]);
-      mfma_next<BF>(st, ot, fq_t[kk]);
+      mfma_next<false>(ss, os, fq_s[kk]);
+      mfma_next<false>(st, ot, fq_t[kk]);
     }
   }
   score_fence(ss, st);
+}
+
+// Eight bfloat16 values to float16, times the power of two s (exact while
+// the result is a normal float16; tiny values round once, huge ones are
+// what s is chosen against).
+__device__ __forceinline__ u16x8 bf16_to_f16_scaled(u16x8 x, float s) {
+  u16x8 out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = __builtin_bit_cast(float, (unsigned)x[e] << 16) * s;
+    out[e] = __builtin_bit_cast(u16, static_cast<_Float16>(v));
+  }
+  return out;
+}
+
+// mask_block with each side's masked logit given (the scores are scaled).
+__device__ __forceinline__ void mask_block_q(f32x16& ss, f32x16& st, unsigned bits, int lim, bool causal,
+                                             float masked_s, float masked_t) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int off = 8 * (r >> 2) + (r & 3);
+    const bool v = ((bits >> off) & 1u) && (!causal || off <= lim);
+    ss[r] = v ? ss[r] : masked_s;
+    st[r] = v ? st[r] : masked_t;
+  }
 }
 
 // Lazy-maximum bound of the fused kernel: every exponential stays below it,
@@ -312,6 +344,9 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
 
   // Negative scales: flip the sign of q (exact) so the effective scale is positive.
   const u16 flip_s = a.s.scale < 0.f ? 0x8000 : 0, flip_t = a.t.scale < 0.f ? 0x8000 : 0;
+  // operands in float16 scaled by 2^-e per side (exact: powers of two)
+  const float k16s = f.k16_scale != nullptr ? *f.k16_scale : 1.f;
+  const float k16t = f.k16t_scale != nullptr ? *f.k16t_scale : 1.f;
   u16x8 fq_s[KS], fq_t[KS];
   {
     const u16* ps = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh + (int64_t)my_i * a.s.q_st;
@@ -320,8 +355,12 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     for (int kk = 0; kk < KS; ++kk) {
       const int d0 = 16 * kk + 8 * half;
       const bool ld = in_range && d0 < a.s.dim;
-      fq_s[kk] = ld ? (*reinterpret_cast<const u16x8*>(ps + d0) ^ flip_s) : (u16x8)(0);
-      fq_t[kk] = ld ? (*reinterpret_cast<const u16x8*>(pt + d0) ^ flip_t) : (u16x8)(0);
+      u16x8 q = ld ? *reinterpret_cast<const u16x8*>(ps + d0) : (u16x8)(0);
+      if constexpr (BF) q = bf16_to_f16_scaled(q, k16s);
+      fq_s[kk] = q ^ flip_s;
+      u16x8 qt = ld ? *reinterpret_cast<const u16x8*>(pt + d0) : (u16x8)(0);
+      if constexpr (BF) qt = bf16_to_f16_scaled(qt, k16t);
+      fq_t[kk] = qt ^ flip_t;
     }
   }
   // The query operands are read-only for the whole loop: they live in AGPRs
@@ -329,12 +368,18 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) asm volatile("" : "+a"(fq_s[kk]), "+a"(fq_t[kk]));
 
-  const float c2s = fabsf(a.s.scale2), c2t = fabsf(a.t.scale2);
-  SoftRow R = {kStartMax, kStartMax, stabiliser(kStartMax, c2s), stabiliser(kStartMax, c2t), 0.f, 0.f, 0.f};
+  // scores come out of the MFMA scaled by 2^-2e: c2 absorbs 4^e
+  const float inv16 = 1.f / k16s, inv16t = 1.f / k16t;  // 2^e, exact
+  const float c2s = fabsf(a.s.scale2) * inv16 * inv16, c2t = fabsf(a.t.scale2) * inv16t * inv16t;
+  // the student's masked logit and start maximum in the same scaled units,
+  // so every product with c2s equals the unscaled one (and stays finite)
+  const float masked_s = kMaskedLogit * k16s * k16s, start_s = kStartMax * k16s * k16s;
+  const float masked_t = kMaskedLogit * k16t * k16t, start_t = kStartMax * k16t * k16t;
+  SoftRow R = {start_s, start_t, stabiliser(start_s, c2s), stabiliser(start_t, c2t), 0.f, 0.f, 0.f};
 
   const int hs = h / a.s.group, ht = h / a.t.group;
-  const u16* ks_base = a.s.k + (int64_t)b * a.s.k_sb + (int64_t)hs * a.s.k_sh;
-  const u16* kt_base = a.t.k + (int64_t)b * a.t.k_sb + (int64_t)ht * a.t.k_sh;
+  const u16* ks_base = f.k16 + (int64_t)b * f.k16_sb + (int64_t)hs * f.k16_sh;
+  const u16* kt_base = f.k16t + (int64_t)b * f.k16t_sb + (int64_t)ht * f.k16t_sh;
   const unsigned char* tok = f.tok_ok + (int64_t)b * f.Tp;
 
   const int nkt_all = f.Tp / kTile;
@@ -345,13 +390,13 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   auto tile_of = [&](int it) { return causal ? ntiles - 1 - it : it; };
   // per-lane copy offsets of a full tile, computed once
   RowCopier<DP, kWavesQ> cp_s, cp_t;
-  cp_s.init((int)a.s.k_st, a.s.dim, w, lane);
-  cp_t.init((int)a.t.k_st, a.t.dim, w, lane);
+  cp_s.init((int)f.k16_st, a.s.dim, w, lane);
+  cp_t.init((int)f.k16t_st, a.t.dim, w, lane);
   auto issue_tile = [&](int it) {
     const int buf = it % kBufs;
     const int j0 = tile_of(it) * kTile;
-    cp_s.issue(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
-    cp_t.issue(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    cp_s.issue(lk[buf][0], ks_base, (int)f.k16_st, j0, T, a.s.dim, w, lane);
+    cp_t.issue(lk[buf][1], kt_base, (int)f.k16t_st, j0, T, a.t.dim, w, lane);
     issue_small(ltok[buf][w], tok + j0, lane);
   };
   unsigned g1off[KS];  // this lane's row chunks of a sub-block: row l32, chunk 2kk + half
@@ -375,7 +420,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
     if (x.tm != ~0ull || (causal && gsb >= diag_sb)) {
       const int first = kt0 + 32 * sb + 4 * half;
-      mask_block(x.s, x.t, (unsigned)(x.tm >> (32 * sb + 4 * half)), my_i - first, causal);
+      mask_block_q(x.s, x.t, (unsigned)(x.tm >> (32 * sb + 4 * half)), my_i - first, causal, masked_s, masked_t);
     }
   };
 
@@ -431,9 +476,9 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       float xt[NPAIR][2], xs[NPAIR][2], dd[NPAIR][2];
       // phase 0: student scores; exponent arguments
       if (kk == 0)
-        mfma_first<BF>(nxt.s, os[0], fq_s[0]);
+        mfma_first<false>(nxt.s, os[0], fq_s[0]);
       else
-        mfma_next<BF>(nxt.s, os[kk], fq_s[kk]);
+        mfma_next<false>(nxt.s, os[kk], fq_s[kk]);
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         const int r = kk * EP + 2 * p;
@@ -446,9 +491,9 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       __builtin_amdgcn_sched_barrier(0);
       // phase 1: teacher scores; differences, teacher exponentials
       if (kk == 0)
-        mfma_first<BF>(nxt.t, ot[0], fq_t[0]);
+        mfma_first<false>(nxt.t, ot[0], fq_t[0]);
       else
-        mfma_next<BF>(nxt.t, ot[kk], fq_t[kk]);
+        mfma_next<false>(nxt.t, ot[kk], fq_t[kk]);
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         const int r = kk * EP + 2 * p;
@@ -460,7 +505,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       }
       __builtin_amdgcn_sched_barrier(0);
       // phase 2: student output product; student exponentials and sums
-      mfma_oacc<BF>(kk * PPK % NDB, o_s[kk * PPK % NDB], oa[kk * PPK], pop_s[kk * PPK / NDB]);
+      mfma_oacc<false>(kk * PPK % NDB, o_s[kk * PPK % NDB], oa[kk * PPK], pop_s[kk * PPK / NDB]);
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         const int r = kk * EP + 2 * p;
@@ -472,7 +517,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       }
       __builtin_amdgcn_sched_barrier(0);
       // phase 3: teacher output product; teacher sums, KL terms, packing
-      mfma_oacc<BF>(NDB + kk * PPK % NDB, o_t[kk * PPK % NDB], oa[kk * PPK], pop_t[kk * PPK / NDB]);
+      mfma_oacc<false>(NDB + kk * PPK % NDB, o_t[kk * PPK % NDB], oa[kk * PPK], pop_t[kk * PPK / NDB]);
 #pragma unroll
       for (int p = 0; p < NPAIR; ++p) {
         const int r = kk * EP + 2 * p;
@@ -480,8 +525,8 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
         t1s += pt[r + 1];
         a0 = fmaf(pt[r], dd[p][0], a0);
         a1 = fmaf(pt[r + 1], dd[p][1], a1);
-        ws[r >> 1] = pack2<BF>(ps[r], ps[r + 1]);
-        wt[r >> 1] = pack2<BF>(pt[r], pt[r + 1]);
+        ws[r >> 1] = pack2<false>(ps[r], ps[r + 1]);
+        wt[r >> 1] = pack2<false>(pt[r], pt[r + 1]);
         asm volatile("" : "+v"(t0), "+v"(t1s), "+v"(a0), "+v"(a1), "+v"(ws[r >> 1]), "+v"(wt[r >> 1]));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -489,8 +534,8 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
 #pragma unroll
       for (int q = 1; q < PPK; ++q) {
         const int j = kk * PPK + q;
-        mfma_oacc<BF>(j % NDB, o_s[j % NDB], oa[j], pop_s[j / NDB]);
-        mfma_oacc<BF>(NDB + j % NDB, o_t[j % NDB], oa[j], pop_t[j / NDB]);
+        mfma_oacc<false>(j % NDB, o_s[j % NDB], oa[j], pop_s[j / NDB]);
+        mfma_oacc<false>(NDB + j % NDB, o_t[j % NDB], oa[j], pop_t[j / NDB]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -500,7 +545,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     float fs = 1.f, ft = 1.f;
     if (raise) {
       raise_max_row(cur.s, cur.t, R, c2s, c2t, fs, ft);
-      bs = block_probs_packed<BF>(cur.s, cur.t, R, c2s, c2t, ws, wt);
+      bs = block_probs_packed<false>(cur.s, cur.t, R, c2s, c2t, ws, wt);
     }
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -551,8 +596,8 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       const u16x8 op = tro.read(t2, k2 & 1, j / NDB, j % NDB);
-      mfma_oacc<BF>(j % NDB, o_s[j % NDB], op, pop_s[j / NDB]);
-      mfma_oacc<BF>(NDB + j % NDB, o_t[j % NDB], op, pop_t[j / NDB]);
+      mfma_oacc<false>(j % NDB, o_s[j % NDB], op, pop_s[j / NDB]);
+      mfma_oacc<false>(NDB + j % NDB, o_t[j % NDB], op, pop_t[j / NDB]);
     }
   }
   agpr_fence<NDB>(o_s, o_t);
@@ -571,8 +616,8 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   const bool one_key = row_valid && (causal ? my_i == f.first2[2 * b] : f.first2[2 * b + 1] >= T);
   const int64_t row_index = (int64_t)bh * T + my_i;
   if (in_range && half == 0) {
-    const float ls = one_key ? mul_rn(ms, fabsf(a.s.scale)) : (l_s > 0.f ? (lg_s - ns) * kLn2 : kNegInf);
-    const float lt = one_key ? mul_rn(mt, fabsf(a.t.scale)) : (l_t > 0.f ? (lg_t - nt) * kLn2 : kNegInf);
+    const float ls = one_key ? mul_rn(ms * inv16 * inv16, fabsf(a.s.scale)) : (l_s > 0.f ? (lg_s - ns) * kLn2 : kNegInf);
+    const float lt = one_key ? mul_rn(mt * inv16t * inv16t, fabsf(a.t.scale)) : (l_t > 0.f ? (lg_t - nt) * kLn2 : kNegInf);
     f.lse_s_out[row_index] = row_valid ? ls : 0.f;
     f.lse_t_out[row_index] = row_valid ? lt : 0.f;
     const float wr = a.weight != nullptr ? *a.weight : 1.f;
@@ -580,8 +625,9 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   }
   if (in_range) {
     const bool g_ok = ok && !one_key;
-    const float fs = g_ok ? a.s.scale / l_s : 0.f;
-    const float ft = g_ok ? a.s.scale / l_t : 0.f;
+    // the products used the scaled keys: sm_scale_s * 2^e / l
+    const float fs = g_ok ? a.s.scale * inv16 / l_s : 0.f;
+    const float ft = g_ok ? a.s.scale * inv16 / l_t : 0.f;
     float* out = f.dq_out + row_index * a.s.dim;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -614,6 +660,11 @@ __global__ __launch_bounds__(kWavesQ * 64) void hot_fwdq_batch_kernel(const HotB
 }
 
 hipError_t launch_hot_fwdq(const HotArgs& f, int dp, bool bf16, hipStream_t stream);
+// bfloat16 inputs, one side: k16 = float16(k * scale) as a contiguous
+// [B, Hkv, T, D] tensor, *scale = the power of two 2^-e chosen against
+// max |q|, |k| (device; maxbits is scratch).
+hipError_t launch_keys_f16(const SideArgs& s, int B, int Hq, int T, unsigned* maxbits, float* scale, u16* k16,
+                           hipStream_t stream);
 hipError_t launch_hot_fwdq_batch(HotBatch& m, int dp, bool bf16, hipStream_t stream);
 
 }  // namespace lard

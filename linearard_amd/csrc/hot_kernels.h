@@ -53,6 +53,15 @@ struct HotArgs {
   float* lse_t_out;
   float* row_out;                // fwd: per-row KL
   float* dq_out;                 // dq: [B, Hq, T, Ds]
+  // Fused row-gradient forward only: each side's keys as float16 (the input
+  // itself for float16 inputs, a scaled copy for bfloat16 ones) and the
+  // device scalar 2^-e they were scaled by (NULL: 1).
+  const u16* k16;  // student
+  int64_t k16_sb, k16_sh, k16_st;
+  const float* k16_scale;
+  const u16* k16t;  // teacher
+  int64_t k16t_sb, k16t_sh, k16t_st;
+  const float* k16t_scale;
 };
 
 // 16 bytes per lane HBM -> LDS: lane l copies base + voff (bytes) to
