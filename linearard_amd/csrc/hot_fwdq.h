@@ -45,6 +45,8 @@
 // reader of tile t-2, whose buffer then receives tile t+2.
 #pragma once
 
+#include <type_traits>
+
 #include "hot_kernels.h"
 
 namespace lard {
@@ -428,7 +430,14 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
 
   // Step k: scores of sub-block k1 into nxt, output products of sub-block
   // k-1 (packed in pop_*), softmax of sub-block k (cur, already scored).
-  auto step = [&](Sub& cur, int k, Sub& nxt, int k1) {
+  // First operands of the next step, read at the end of the current one so
+  // the next step's first MFMAs need not wait for LDS: the output-product
+  // operand (sub-block k, always resident) after every step, the score
+  // operands (sub-block k+2) only after odd steps, whose next step scores a
+  // tile that landed before the barrier preceding the odd step.
+  u16x8 pre_os = (u16x8)(0), pre_ot = (u16x8)(0), pre_oa = (u16x8)(0);
+  auto step = [&](Sub& cur, int k, Sub& nxt, int k1, auto pre1_in, auto pre1_out) {
+    constexpr bool PRE1_IN = decltype(pre1_in)::value, PRE1_OUT = decltype(pre1_out)::value;
     prepare(cur, k);
     const int b1 = buf_of(k1);
     nxt.tm = __ballot(ltok[b1][w][lane] != 0);
@@ -446,10 +455,14 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       ot[kk] = *reinterpret_cast<const u16x8*>(p + kTile * DP);
     };
     auto load2 = [&](int j) { oa[j] = tro.read(t2, sb2, j / NDB, j % NDB); };
-#pragma unroll
-    for (int kk = 0; kk < PD && kk < KS; ++kk) load1(kk);
-#pragma unroll
-    for (int j = 0; j < PA && j < NP; ++j) load2(j);
+    static_assert(PD == 1 && PA == 1, "the carried operands are the first k-step's");
+    if constexpr (PRE1_IN) {
+      os[0] = pre_os;
+      ot[0] = pre_ot;
+    } else {
+      load1(0);
+    }
+    oa[0] = pre_oa;
 
     float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1s = 0.f, a0 = 0.f, a1 = 0.f;
     float ps[16], pt[16];
@@ -472,6 +485,14 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       for (int q = 0; q < PPK; ++q) {
         const int j = kk * PPK + q;
         if (j + PA < NP) load2(j + PA);
+      }
+      if (kk == KS - 1) {  // the next step's first operands
+        pre_oa = tro.read(lk[buf_of(k)][0], k & 1, 0, 0);
+        if constexpr (PRE1_OUT) {
+          const u16* p = lk[buf_of(k + 2)][0] + 32 * (k & 1) * DP + g1off[0];  // sub-block k+2 has k's half
+          pre_os = *reinterpret_cast<const u16x8*>(p);
+          pre_ot = *reinterpret_cast<const u16x8*>(p + kTile * DP);
+        }
       }
       float xt[NPAIR][2], xs[NPAIR][2], dd[NPAIR][2];
       // phase 0: student scores; exponent arguments
@@ -541,7 +562,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     }
     score_fence(nxt.s, nxt.t);
     BlockSums bs = {s0 + s1, t0 + t1s, a0 + a1};
-    const bool raise = __any(!(bs.s <= kLazySumQ) || !(bs.t <= kLazySumQ));
+    const bool raise = __any(!(fmaxf(bs.s, bs.t) <= kLazySumQ));  // sums are never NaN; +inf raises
     float fs = 1.f, ft = 1.f;
     if (raise) {
       raise_max_row(cur.s, cur.t, R, c2s, c2t, fs, ft);
@@ -573,8 +594,14 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   Sub A, B;
   A.tm = __ballot(ltok[0][w][lane] != 0);
   sub_scores_q<DP, BF>(lk[0][0], 0, l32, half, fq_s, fq_t, A.s, A.t);
+  {  // what step 0 would have carried: scores of sub-block 1, products of "sub-block -1" (zero operands)
+    const u16* p = lk[0][0] + 32 * DP + g1off[0];
+    pre_os = *reinterpret_cast<const u16x8*>(p);
+    pre_ot = *reinterpret_cast<const u16x8*>(p + kTile * DP);
+    pre_oa = tro.read(lk[0][0], 0, 0, 0);
+  }
   for (int k = 0; k < nsub; k += 2) {
-    step(A, k, B, k + 1);
+    step(A, k, B, k + 1, std::true_type{}, std::false_type{});
     // barrier before step 2t-1 = k+1 (t = k/2 + 1): tile t landed, tile t-2 free
     const int t = (k >> 1) + 1;
     if (t < ntiles) {
@@ -587,7 +614,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     }
     // the last step recomputes the scores of the last sub-block (still in
     // LDS) and drops them: one code path for every step
-    step(B, k + 1, A, min(k + 2, nsub - 1));
+    step(B, k + 1, A, min(k + 2, nsub - 1), std::false_type{}, std::true_type{});
   }
   // output products of the last sub-block
   {
