@@ -125,11 +125,13 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
 
 /*
  * Which kernels lard_attn_kl_forward / lard_attn_kl_backward run for these
- * operands: a LARD_PATH_* value (>= 0), or a negative error for invalid
- * operands.  After a non-throughput answer, lard_last_error() names the
- * condition (head dims differ or exceed 128, dtypes differ, a head of 2^30
- * elements or more, scales outside [1e-6, 1e6] or more than 1e6 apart,
- * float32); it is empty for LARD_PATH_THROUGHPUT.  No counterpart in the
+ * operands: a LARD_PATH_* value (>= 0), or the negative error that
+ * lard_attn_kl_forward would return for invalid operands (q/k pairs that do
+ * not match, student and teacher B/Hq/T that differ, float32 on one side
+ * only, scales that are not finite).  After a non-throughput answer,
+ * lard_last_error() names the condition (head dims differ or exceed 128,
+ * dtypes differ, a head of 2^30 elements or more, scales outside
+ * [1e-6, 1e6] or more than 1e6 apart, float32); it is empty for LARD_PATH_THROUGHPUT.  No counterpart in the
  * reference (one Triton path, kernel_A.py / kernel_B.py / kernel_C.py); it
  * lets a caller see the slower paths the reference does not have.
  */

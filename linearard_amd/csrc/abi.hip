@@ -608,6 +608,10 @@ int lard_attn_kl_path(const lard_tensor4* qs, const lard_tensor4* ks, const lard
   int rc;
   if ((rc = check_pair(qs, ks, "qs", "ks")) != LARD_OK) return rc;
   if ((rc = check_pair(qt, kt, "qt", "kt")) != LARD_OK) return rc;
+  if (qs->size[0] != qt->size[0] || qs->size[1] != qt->size[1] || qs->size[2] != qt->size[2])
+    return fail(LARD_ERR_INVALID_ARGUMENT, "student/teacher B/Hq/T must align");
+  if ((qs->dtype == LARD_DTYPE_F32) != (qt->dtype == LARD_DTYPE_F32))
+    return fail(LARD_ERR_UNSUPPORTED, "float32 inputs need float32 on both sides");
   if ((rc = check_scale(sm_scale_s, "sm_scale_s")) != LARD_OK) return rc;
   if ((rc = check_scale(sm_scale_t, "sm_scale_t")) != LARD_OK) return rc;
   std::string why;

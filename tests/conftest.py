@@ -19,3 +19,14 @@ def gpu_available():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible to torch")
     return True
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Print the achieved parity errors of every check that ran."""
+    from tests._tolerance import summary_lines
+
+    lines = summary_lines()
+    if lines:
+        terminalreporter.section("parity errors")
+        for ln in lines:
+            terminalreporter.write_line(ln)

@@ -327,3 +327,11 @@ def test_attn_kl_path_names_the_slower_paths_without_a_gpu():
     assert rc == 1 and "2^30" in why
     rc, why = path(desc(D=24), desc(D=24))
     assert rc == -2 and "supported set" in why  # invalid operands: an error, as for the compute calls
+    # the alignment checks of the compute calls, with their error codes
+    rc, why = path(desc(dtype=2), desc(dtype=1))
+    assert rc == -2 and "float32 on both sides" in why
+    rc, why = path(desc(dtype=1), desc(dtype=2))
+    assert rc == -2 and "float32 on both sides" in why
+    for kw in ({"T": 128}, {"H": 4}):
+        rc, why = path(desc(), desc(**kw))
+        assert rc == -1 and "B/Hq/T must align" in why

@@ -24,7 +24,7 @@ import pytest
 
 from oracle import attn_kl as O
 from tests._inputs import to_dev
-from tests._tolerance import _grad_ok, _logit_bound, _loss_ok
+from tests._tolerance import check_grad, check_loss
 
 pytestmark = pytest.mark.gpu
 
@@ -61,9 +61,9 @@ def test_rising_logits_take_the_rescale_path(gpu_available, D, causal):
     loss = attn_kl_align(x_s, x_s, to_dev(xt, dtype), to_dev(xt, dtype), causal=causal, sm_scale_s=a, sm_scale_t=a)
     loss.backward()
     rl, rdx, _, _, _ = O.attn_kl_align(xs, xs, xt, xt, None, causal, a, a, self_relation=True)
-    lb = _logit_bound((xs, xs, a), (xt, xt, a))
     assert rl > 1e-2 * 2 * T, rl  # a real KL, not the fp32 floor of the gate
-    assert np.isfinite(loss.item()) and _loss_ok(loss.item(), rl, 2 * T, lb), (loss.item(), rl)
+    assert np.isfinite(loss.item())
+    check_loss(loss.item(), rl, f"rescale-D{D}-c{int(causal)}")
     g_dx = x_s.grad.float().cpu().numpy()
     assert np.isfinite(g_dx).all()
-    assert _grad_ok(g_dx, rdx, xs, a, lb)
+    check_grad(g_dx, rdx, f"rescale-D{D}-c{int(causal)}")

@@ -19,7 +19,7 @@ import torch
 
 from oracle import attn_kl as O
 from tests._inputs import make_mask, mask_to_dev, randn, to_dev
-from tests._tolerance import _grad_ok, _logit_bound, _loss_ok
+from tests._tolerance import check_grad, check_loss
 
 pytestmark = pytest.mark.gpu
 
@@ -45,6 +45,7 @@ CASES = [
 def test_autograd_sweep(gpu_available, case):
     from linearard_amd.attention_KL import attn_kl_align
 
+    cid = "sweep-" + "-".join(str(c) for c in case)
     dtype, B, Hq, Hkv, T, D, ratio, causal, sr, self_rel = case
     rng = np.random.default_rng(1000 + 7 * T + Hq + D)
     a_s = 1 / math.sqrt(D)
@@ -62,9 +63,8 @@ def test_autograd_sweep(gpu_available, case):
                              sm_scale_t=a_t)
         loss.backward()
         rl, rdx, _, _, _ = O.attn_kl_align(xs, xs, xt, xt, mask, causal, a_s, a_t, self_relation=True)
-        lb = _logit_bound((xs, xs, a_s), (xt, xt, a_t))
-        assert _loss_ok(loss.item(), rl, B * Hq * T, lb), (loss.item(), rl)
-        assert _grad_ok(x_s.grad.float().cpu().numpy(), rdx, xs, a_s, lb)
+        check_loss(loss.item(), rl, cid)
+        check_grad(x_s.grad.float().cpu().numpy(), rdx, cid)
     else:
         qt = randn(rng, (B, Hq, T, D), dtype)
         kt = randn(rng, (B, Hkv, T, D), dtype)
@@ -75,10 +75,9 @@ def test_autograd_sweep(gpu_available, case):
                              causal=causal, sm_scale_s=a_s, sm_scale_t=a_t)
         loss.backward()
         rl, rdq, rdk, _, _ = O.attn_kl_align(qs, ks, qt, kt, mask, causal, a_s, a_t)
-        lb = _logit_bound((qs, ks, a_s), (qt, kt, a_t))
-        assert _loss_ok(loss.item(), rl, B * Hq * T, lb), (loss.item(), rl)
-        assert _grad_ok(tqs.grad.float().cpu().numpy(), rdq, ks, a_s, lb)
-        assert _grad_ok(tks.grad.float().cpu().numpy(), rdk, qs, a_s, lb)
+        check_loss(loss.item(), rl, cid)
+        check_grad(tqs.grad.float().cpu().numpy(), rdq, cid, "dq")
+        check_grad(tks.grad.float().cpu().numpy(), rdk, cid, "dk")
     # No valid token (kernel_A.py:157-158, kernel_C.py:252-256), one kept token
     # or T = 1: every valid row has a single key, so P_s = P_t = 1 there and the
     # reference's lse == S makes its KL and D exactly 0 (kernel_A.py:147-157,
