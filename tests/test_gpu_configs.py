@@ -25,6 +25,7 @@ import torch
 
 import bench
 from oracle import attn_kl as O
+from tests._tolerance import check_grad, check_loss
 
 pytestmark = pytest.mark.gpu
 
@@ -41,19 +42,18 @@ def _fwd_bwd(xs, xt, a, mask=None):
     return loss.detach(), x.grad
 
 
-def _check_head(xs, xt, b, h, a, loss_h, grad_h, dtype, chunk=1024, mask_b=None):
+def _check_head(name, xs, xt, b, h, a, loss_h, grad_h, dtype, chunk=1024, mask_b=None):
     x_s = xs[b, h].float().cpu().numpy()
     x_t = xt[b, h].float().cpu().numpy()
     ref_loss, ref_dx, _, _, kl_rows = O.self_relation_chunked(x_s, x_t, True, a, a, mask=mask_b, chunk=chunk,
                                                               dtype=dtype)
     assert kl_rows.min() >= -1e-6, kl_rows.min()  # KL >= 0 per row
-    assert abs(loss_h - ref_loss) <= LOSS_RTOL * abs(ref_loss), (b, h, loss_h, ref_loss)
-    got = grad_h.float().cpu().numpy()
-    err = np.abs(got - ref_dx).max() / np.abs(ref_dx).max()
-    assert err <= GRAD_RTOL, (b, h, err)
+    case = f"{name}-b{b}h{h}"
+    check_loss(loss_h, ref_loss, case, bar=LOSS_RTOL)
+    check_grad(grad_h.float().cpu().numpy(), ref_dx, case, bar=GRAD_RTOL)
 
 
-def _relation(xs, xt, a, heads, mask=None, dtype=np.float32):
+def _relation(name, xs, xt, a, heads, mask=None, dtype=np.float32):
     """The whole relation in one launch; `heads` = [(b, h)] checked against
     the oracle through single-head launches whose gradients must equal the
     full launch's bitwise."""
@@ -69,7 +69,7 @@ def _relation(xs, xt, a, heads, mask=None, dtype=np.float32):
             total += lh.double().item()
             if (b, h) in heads:
                 mb = None if mask is None else mask[b].cpu().numpy()
-                _check_head(xs, xt, b, h, a, lh.double().item(), dh[0, 0], dtype, mask_b=mb)
+                _check_head(name, xs, xt, b, h, a, lh.double().item(), dh[0, 0], dtype, mask_b=mb)
     assert abs(loss.double().item() - total) <= 1e-5 * abs(total), (loss.item(), total)
     return loss
 
@@ -84,9 +84,9 @@ def test_cfg2_true_outliers_against_the_oracle(gpu_available):
     xs, xt = rel["q"]
     x0 = xt[0, 0].float()
     assert float((a * (x0 * x0).sum(-1)).max()) > 100.0  # really the large-logit regime
-    _relation(xs, xt, a, heads={(0, 0), (0, 31)}, dtype=np.float64)
+    _relation("cfg2-q", xs, xt, a, heads={(0, 0), (0, 31)}, dtype=np.float64)
     xs, xt = rel["k"]
-    _relation(xs, xt, a, heads={(0, 7)}, dtype=np.float64)
+    _relation("cfg2-k", xs, xt, a, heads={(0, 7)}, dtype=np.float64)
     v, _ = rel["v"]
     lv, dv = _fwd_bwd(v, v, a)
     assert lv.item() == 0.0 and not bool(dv.any())
@@ -101,8 +101,8 @@ def test_cfg3_own_inputs_against_the_oracle(gpu_available):
 
     rel = bench.config_relations("cfg3", seed=3)
     a = 1 / math.sqrt(128)
-    _relation(*rel["q"], a, heads={(0, 5)})
-    _relation(*rel["k"], a, heads={(0, 3)})
+    _relation("cfg3-q", *rel["q"], a, heads={(0, 5)})
+    _relation("cfg3-k", *rel["k"], a, heads={(0, 3)})
     v, _ = rel["v"]
     lv, dv = _fwd_bwd(v, v, a)
     assert lv.item() == 0.0 and not bool(dv.any())
@@ -127,7 +127,7 @@ def test_cfg4_bench_inputs_against_the_oracle(gpu_available):
     pre-RoPE N(0,1), teacher RoPE at p, student at p/8; head 0 against the
     chunked float32 oracle, every head by head independence."""
     rel = bench.config_relations("cfg4")
-    _relation(*rel["q"], 1 / math.sqrt(128), heads={(0, 0)})
+    _relation("cfg4-q", *rel["q"], 1 / math.sqrt(128), heads={(0, 0)})
 
 
 def test_cfg5_layer_against_the_oracle(gpu_available):
@@ -145,9 +145,9 @@ def test_cfg5_layer_against_the_oracle(gpu_available):
     assert mask.dtype == torch.int64 and bool((mask == 1).all())
     # float64 oracle: the Student-t channels give large logits, where a float32
     # oracle's own per-row KL already goes negative by ~1e-6
-    _relation(*rel["q"], a, heads={(0, 11)}, mask=mask, dtype=np.float64)
-    _relation(*rel["k"], a, heads={(1, 2)}, mask=mask, dtype=np.float64)
-    _relation(*rel["v"], a, heads={(0, 6)}, mask=mask, dtype=np.float64)
+    _relation("cfg5-q", *rel["q"], a, heads={(0, 11)}, mask=mask, dtype=np.float64)
+    _relation("cfg5-k", *rel["k"], a, heads={(1, 2)}, mask=mask, dtype=np.float64)
+    _relation("cfg5-v", *rel["v"], a, heads={(0, 6)}, mask=mask, dtype=np.float64)
 
     s1 = [rel[k][0].detach().clone().requires_grad_(True) for k in "qkv"]
     t = [rel[k][1] for k in "qkv"]

@@ -1,14 +1,27 @@
-"""GPU parity of distillation_loss with the reference's loss lines
-(train.py:360-423) written out literally over attn_kl_align and torch ops."""
+"""GPU parity of distillation_loss (train.py:360-423) against the CPU oracles.
+
+The relation terms come from oracle.attn_kl (float64: attn_kl_align for the
+small case, the chunked self-relation restatement at cfg5's length), the
+logits term from oracle.logits_kl; the bars are the north star's
+(tests/_tolerance.py).  At cfg5's launch shape (8 relations of each kind per
+batched launch, B=2, n=16384) one head per relation is checked against the
+oracle and the others through properties that hold at any size: a head's
+gradient in the full step equals a launch of that head alone, and the
+losses are sums over relations and heads.
+"""
 
 import math
 
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
+import bench
+from oracle import attn_kl as O
+from oracle import logits_kl as OL
 from tests._inputs import make_mask, mask_to_dev
+from tests._oracle_pool import oracle_heads
+from tests._tolerance import _rel, check_grad, check_loss
 
 pytestmark = pytest.mark.gpu
 
@@ -21,96 +34,66 @@ def _layers(g, L, B, T, D, Hq, Hkv):
     return [[pair(Hq), pair(Hkv), pair(Hkv)] for _ in range(L)]
 
 
-def _leaves(layers):
-    s = [[p[0].clone().requires_grad_(True) for p in layer] for layer in layers]
-    t = [[p[1] for p in layer] for layer in layers]
-    return s, t
+def _np(x):
+    return x.detach().float().cpu().numpy()
 
 
-def _reference(s, t, t_logits, s_logits, mask, lam_A, lam_L, T, scale):
-    """train.py:360-423 with this package's attn_kl_align for the relation KL
-    and torch float32 for the logits lines (on the bf16-rounded x * (1/T)
-    the reference's `t_logits / T` produces)."""
-    from linearard_amd.attention_KL import attn_kl_align
-
-    Q = K = V = 0.0
-    L = len(s)
-    for l in range(L):
-        (qs, ks, vs), (qt, kt, vt) = s[l], t[l]
-        lq = attn_kl_align(qs, qs, qt, qt, attn_mask=mask, causal=True, sm_scale_s=scale, sm_scale_t=scale)
-        lk = attn_kl_align(ks, ks, kt, kt, attn_mask=mask, causal=True, sm_scale_s=scale, sm_scale_t=scale)
-        lv = attn_kl_align(vs, vs, vt, vt, attn_mask=mask, causal=True, sm_scale_s=scale, sm_scale_t=scale)
-        if mask is None:
-            denom = qs.shape[0] * qs.shape[1] * qs.shape[2]
-        else:
-            denom = mask.sum().clamp_min(1) * qs.shape[1]
-        Q = Q + lq / denom
-        K = K + lk / denom
-        V = V + lv / denom
-    attn = (Q + K + V) / max(1, L)
-    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(T, dtype=torch.float32)
-    # s_logits may be a float32 copy (for a float32 gradient): the value is
-    # rounded as the bf16 tensor op rounds it, the gradient passes in float32
-    # (a .to(bfloat16) in the graph would round the gradient to bf16 as well)
-    def scaled(x):
-        y = x.float() * inv.item()
-        return y + (y.to(torch.bfloat16).float() - y).detach()
-
-    qt_ = scaled(t_logits)
-    qs_ = scaled(s_logits)
-    t_logp = F.log_softmax(qt_, dim=-1)
-    s_logp = F.log_softmax(qs_, dim=-1)
-    logits = (t_logp.exp() * (t_logp - s_logp)).sum(dim=-1).mean()
-    # float32 rounding scales of the logits KL (KL = E[q_t - q_s] - lse_t + lse_s)
-    # and of its gradient c (p_s - p_t) per element
-    lscale = (1 + torch.logsumexp(qt_, -1).abs() + torch.logsumexp(qs_, -1).abs()
-              + (t_logp.exp() * (qt_ - qs_).abs()).sum(-1)).mean().item()
-    kl_rows = (t_logp.exp() * (t_logp - s_logp)).sum(-1, keepdim=True)
-    c = lam_L / (t_logits.shape[0] * t_logits.shape[1]) * inv.item()
-    gscale = (c * (t_logp.exp() + s_logp.exp()) * (1 + t_logp.abs() + s_logp.abs() + kl_rows.abs())).detach()
-    return (lam_A * attn + lam_L * logits, attn, logits, Q, K, V), lscale, gscale
+def _oracle_step(layers, t_logits, s_logits, mask, lam_A, lam_L, T, scale):
+    """train.py:360-423 on the CPU: the relation KLs and their gradients from
+    oracle.attn_kl (float64), the logits KL from oracle.logits_kl.
+    Returns (loss, attn, logits, Q, K, V) and the gradients of the student
+    projections ([layer][q, k, v]) and of s_logits."""
+    L = len(layers)
+    sums = [0.0, 0.0, 0.0]
+    grads = []
+    for layer in layers:
+        B, Hq, Tn, _ = layer[0][0].shape
+        denom = B * Hq * Tn if mask is None else max(int(mask.sum()), 1) * Hq  # train.py:403-406
+        g_layer = []
+        for j, (xs, xt) in enumerate(layer):
+            loss, dx, _, _, _ = O.attn_kl_align(_np(xs), _np(xs), _np(xt), _np(xt), mask, True, scale, scale,
+                                                self_relation=True)
+            sums[j] += loss / denom
+            g_layer.append(dx * (lam_A / max(1, L) / denom))
+        grads.append(g_layer)
+    attn = sum(sums) / max(1, L)
+    logits, _, _, _ = OL.logits_kl(_np(t_logits), _np(s_logits), T, "bf16")
+    _, g_logits = OL.logits_kl_grads(_np(t_logits), _np(s_logits), T, "bf16", dloss=lam_L)
+    return (lam_A * attn + lam_L * logits, attn, logits, *sums), grads, g_logits
 
 
 @pytest.mark.parametrize("ratio,lam_L,T", [(0.2, 0.3, 1.5), (None, 0.5, 1.0)])
-def test_distillation_loss_is_the_train_py_loss(gpu_available, ratio, lam_L, T):
+def test_distillation_loss_against_the_oracle(gpu_available, ratio, lam_L, T):
+    """Three layers (Q/Q 4 heads, K/K and V/V 2, n=96, d=64) and a [2, 8, 1000]
+    logits pair: every returned loss and every student gradient against the
+    float64 oracles."""
     from linearard_amd.distill import distillation_loss
 
     g = torch.Generator(device="cuda").manual_seed(7)
     L, B, Tn, D, Hq, Hkv = 3, 2, 96, 64, 4, 2
     layers = _layers(g, L, B, Tn, D, Hq, Hkv)
-    mask = mask_to_dev(None if ratio is None else make_mask(np.random.default_rng(1), B, Tn, ratio))
+    mask_np = None if ratio is None else make_mask(np.random.default_rng(1), B, Tn, ratio)
+    mask = mask_to_dev(mask_np)
     t_logits = (3 * torch.randn((B, 8, 1000), device="cuda", generator=g)).to(torch.bfloat16)
-    s_logits0 = (t_logits.float() + torch.randn(t_logits.shape, device="cuda", generator=g)).to(torch.bfloat16)
+    s_logits = (t_logits.float() + torch.randn(t_logits.shape, device="cuda", generator=g)).to(torch.bfloat16)
     scale = 1 / math.sqrt(D)
 
-    s1, t1 = _leaves(layers)
-    sl1 = s_logits0.clone().requires_grad_(True)
-    out = distillation_loss([x[0] for x in s1], [x[1] for x in s1], [x[2] for x in s1],
-                            [x[0] for x in t1], [x[1] for x in t1], [x[2] for x in t1],
-                            t_logits, sl1, attn_mask=mask, lam_A=0.7, lam_L=lam_L, temperature=T)
+    s = [[p[0].clone().requires_grad_(True) for p in layer] for layer in layers]
+    t = [[p[1] for p in layer] for layer in layers]
+    sl = s_logits.clone().requires_grad_(True)
+    out = distillation_loss([x[0] for x in s], [x[1] for x in s], [x[2] for x in s],
+                            [x[0] for x in t], [x[1] for x in t], [x[2] for x in t],
+                            t_logits, sl, attn_mask=mask, lam_A=0.7, lam_L=lam_L, temperature=T)
     out.loss.backward()
 
-    s2, t2 = _leaves(layers)
-    sl2 = s_logits0.float().clone().requires_grad_(True)
-    ref, lscale, gscale = _reference(s2, t2, t_logits, sl2, mask, 0.7, lam_L, T, scale)
-    ref[0].backward()
-
-    # attention terms: the same kernels, summed in another order (relative 2e-5);
-    # the logits term: float32 against float32 (2e-5 of its rounding scale)
-    tol_attn = 2e-5 * abs(float(ref[1])) + 1e-8
-    tol_logits = 2e-5 * lscale
-    tols = [0.7 * tol_attn + lam_L * tol_logits, tol_attn, tol_logits] + [2e-5 * abs(float(x)) + 1e-8 for x in ref[3:]]
-    for name, got, want, tol in zip(out._fields, out, ref, tols):
-        assert abs(float(got) - float(want)) <= tol, (name, float(got), float(want), tol)
-    for a, b in zip([x for layer in s1 for x in layer], [x for layer in s2 for x in layer]):
-        err = (a.grad.float() - b.grad.float()).abs().max().item()
-        assert err <= 4e-3 * b.grad.float().abs().max().item() + 1e-9  # same kernels; the bf16 cast may flip
-    # the logits gradient: bf16 output against torch's float32 autograd
-    want = sl2.grad
-    err = (sl1.grad.float() - want).abs()
-    # both sides carry float32 errors of that scale (torch's float32 log_softmax too): 2e-5
-    bound = 2.0 ** -8 * want.abs() + 2e-5 * gscale + 1e-30
-    assert bool((err <= bound).all()), float((err / bound).max())
+    ref, ref_grads, ref_gl = _oracle_step(layers, t_logits, s_logits, mask_np, 0.7, lam_L, T, scale)
+    case = f"distill-L3-r{ratio}-T{T}"
+    for name, got, want in zip(out._fields, out, ref):
+        check_loss(float(got), want, f"{case}-{name}")
+    for l in range(L):
+        for j, kind in enumerate("qkv"):
+            check_grad(_np(s[l][j].grad), ref_grads[l][j], f"{case}-layer{l}", f"d{kind}")
+    check_grad(_np(sl.grad), ref_gl, case, "dlogit")
 
 
 def test_lam_L_zero_logs_the_logits_kl_without_a_gradient_pass(gpu_available):
@@ -119,7 +102,8 @@ def test_lam_L_zero_logs_the_logits_kl_without_a_gradient_pass(gpu_available):
 
     g = torch.Generator(device="cuda").manual_seed(8)
     layers = _layers(g, 2, 1, 64, 32, 2, 1)
-    s, t = _leaves(layers)
+    s = [[p[0].clone().requires_grad_(True) for p in layer] for layer in layers]
+    t = [[p[1] for p in layer] for layer in layers]
     t_logits = torch.randn((1, 4, 512), device="cuda", generator=g).to(torch.bfloat16)
     s_logits = torch.randn((1, 4, 512), device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
     out = distillation_loss([x[0] for x in s], [x[1] for x in s], [x[2] for x in s],
@@ -132,3 +116,86 @@ def test_lam_L_zero_logs_the_logits_kl_without_a_gradient_pass(gpu_available):
     none = distillation_loss([x[0] for x in s], [x[1] for x in s], [x[2] for x in s],
                              [x[0] for x in t], [x[1] for x in t], [x[2] for x in t])
     assert none.logits_loss is None and float(none.loss) == float(out.attn_loss)
+
+
+# ---------------------------------------------------------------------------
+# cfg5's launch shape
+# ---------------------------------------------------------------------------
+
+def test_distillation_step_at_the_cfg5_launch_shape(gpu_available):
+    """Eight cfg5 layers (B=2, n=16384, d=128, bf16; Q/Q 32 heads, K/K and V/V
+    8; all-ones int64 mask; Student-t(3) channels; RoPE base 1e4, student
+    p/4): each kind is one batched launch of 8 relations, the launch shape of
+    the 32-layer cfg5 step (4 launches of 8 per kind).
+
+    * one head of every Q/Q relation (both sequences), one K/K and one V/V
+      head against the float64 chunked oracle: the head's loss (a launch of
+      that head alone) and its gradient inside the full step;
+    * every Q/Q head: its gradient in the full step equals, bitwise, a
+      fwd+bwd launch of that head alone with the step's upstream gradient,
+      and its single-head losses sum to the relation's loss;
+    * Q_loss, K_loss, V_loss are the per-relation launches' losses over the
+      denominator (train.py:403-410), attn their mean.
+    """
+    from linearard_amd.attention_KL import attn_kl_align
+    from linearard_amd.distill import distillation_loss
+
+    L, B, n, Hq = 8, 2, 16384, 32
+    a = 1 / math.sqrt(128)
+    rels = [bench.config_relations("cfg5", seed=500 + l) for l in range(L)]
+    mask = rels[0]["mask"]
+    s = {k: [r[k][0].detach().clone().requires_grad_(True) for r in rels] for k in "qkv"}
+    t = {k: [r[k][1] for r in rels] for k in "qkv"}
+    del rels
+    # bf16 values below 2^15 are float16 values: the kernels' float16 keys
+    # then need no scaling, per relation or per head alike
+    assert max(float(x.detach().abs().max()) for k in "qkv" for x in s[k] + t[k]) < 2.0 ** 15
+
+    print("cfg5 launch shape: distillation_loss over 8 layers", flush=True)
+    out = distillation_loss(s["q"], s["k"], s["v"], t["q"], t["k"], t["v"], attn_mask=mask)
+    out.loss.backward()
+    torch.cuda.synchronize()
+    denom = float(mask.sum()) * Hq                     # train.py:405-406
+    c = 1.0 / L / denom                                # lam_A = 1: d loss / d relation loss
+    assert c == 2.0 ** -23
+
+    picks = [("q", l, l % 2, (7 * l + 3) % Hq) for l in range(L)] + [("k", 3, 1, 5), ("v", 6, 0, 2)]
+    jobs = [(_np(s[k][l][b, h]).astype(np.float64), _np(t[k][l][b, h]).astype(np.float64), a,
+             mask[b].cpu().numpy()) for k, l, b, h in picks]
+    print(f"cfg5 launch shape: {len(jobs)} oracle heads on the CPU", flush=True)
+    refs = oracle_heads(jobs)
+    for (k, l, b, h), (ref_loss, ref_dx, kl_min) in zip(picks, refs):
+        assert kl_min >= -1e-9, kl_min  # the oracle's per-row KL >= 0
+        with torch.no_grad():
+            lh = attn_kl_align(s[k][l][b:b + 1, h:h + 1].detach(), s[k][l][b:b + 1, h:h + 1].detach(),
+                               t[k][l][b:b + 1, h:h + 1], t[k][l][b:b + 1, h:h + 1], attn_mask=mask[b:b + 1],
+                               causal=True, sm_scale_s=a, sm_scale_t=a)
+        case = f"cfg5-step-{k}{l}-b{b}h{h}"
+        check_loss(lh.item(), ref_loss, case)
+        check_grad(_np(s[k][l].grad[b, h]), c * ref_dx, case, f"d{k}")
+
+    print("cfg5 launch shape: single-head launches of every Q/Q head", flush=True)
+    for l in range(L):
+        total = 0.0
+        for b in range(B):
+            for h in range(Hq):
+                x = s["q"][l][b:b + 1, h:h + 1].detach().clone().requires_grad_(True)
+                xt = t["q"][l][b:b + 1, h:h + 1]
+                lh = attn_kl_align(x, x, xt, xt, attn_mask=mask[b:b + 1], causal=True, sm_scale_s=a, sm_scale_t=a)
+                lh.backward(torch.tensor(c, device="cuda"))
+                assert torch.equal(x.grad[0, 0], s["q"][l].grad[b, h]), f"Q/Q relation {l} head ({b}, {h})"
+                total += lh.double().item()
+        with torch.no_grad():
+            lr = attn_kl_align(s["q"][l].detach(), s["q"][l].detach(), t["q"][l], t["q"][l], attn_mask=mask,
+                               causal=True, sm_scale_s=a, sm_scale_t=a).double().item()
+        assert _rel(lr, total) <= 1e-5, (l, lr, total)
+
+    sums = {}
+    for k in "qkv":
+        with torch.no_grad():
+            sums[k] = sum(attn_kl_align(x.detach(), x.detach(), y, y, attn_mask=mask, causal=True, sm_scale_s=a,
+                                        sm_scale_t=a).double().item() for x, y in zip(s[k], t[k])) / denom
+    for k, got in (("q", out.Q_loss), ("k", out.K_loss), ("v", out.V_loss)):
+        assert _rel(got.item(), sums[k]) <= 1e-5, (k, got.item(), sums[k])
+    attn = (sums["q"] + sums["k"] + sums["v"]) / L
+    assert _rel(out.attn_loss.item(), attn) <= 1e-5 and out.loss.item() == out.attn_loss.item()

@@ -123,7 +123,7 @@ def test_padding_mask_at_16k_against_the_oracle(gpu_available):
     mask[1] = rng.random(n) > 0.1
     mask[1, 0] = 1
     m = torch.tensor(mask, device="cuda")
-    _relation(xs, xt, a, heads={(0, 1), (1, 3)}, mask=m)
+    _relation("pad16k", xs, xt, a, heads={(0, 1), (1, 3)}, mask=m)
     _, dx = _fwd_bwd_masked(xs, xt, a, m)
     assert not bool(dx[0, :, n - 2500:].any())
     assert not bool(dx[1][:, torch.tensor(mask[1] == 0, device="cuda")].any())
