@@ -29,6 +29,7 @@ copy of known size), else null.
     python bench.py --workload rope                  # RoPE pair producer, HBM roofline
     python bench.py --workload logits                # logits KL (train.py:412-420), HBM roofline
     python bench.py --workload step --steps 2 --warmup 1   # cfg5 distillation-step loss (32 layers)
+    python bench.py --workload stages                # stage A / B / C entry points, reference gate shapes
 """
 
 from __future__ import annotations
@@ -313,6 +314,80 @@ def run_layers(args):
     }))
 
 
+def run_stages(args):
+    """The three stage entry points (lard_lse_stats, lard_kl_forward,
+    lard_kl_backward) at the reference's own utilisation-gate shapes, fp16,
+    non-causal, no mask (kernels/attention_KL/test_kernel_A.py:282-308,
+    test_kernel_B.py:324-354, test_kernel_C.py:375-405):
+
+      A  lse_stats    B=8, Hq=16, Hkv=4, T=2048, D=128
+      B  kl_forward   B=8, Hq=16, Hkv_s=4, Hkv_t=2, T=2048, Ds=Dt=128
+      C  kl_backward  as B with Ds=8 (dq and dk of the student, float32)
+
+    Each stage is timed alone: `--steps` calls after `--warmup`, bracketed
+    by events on the launch stream.  Algorithmic flops per (b, hq) with
+    P = T^2 pairs: A 2*D*P (S = Q K^T), B 2*(Ds+Dt)*P (S_s and S_t), C
+    2*(Ds+Dt)*P + 4*Ds*P (the recomputed S_s, S_t and dq = D K_s,
+    dk = D^T Q_s)."""
+    import torch
+
+    from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
+
+    B, Hq, T = 8, 16, 2048
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(2)
+
+    def draw(H, D):
+        return torch.randn((B, H, T, D), generator=g).to(torch.float16).to(dev)
+
+    q, k = draw(Hq, 128), draw(4, 128)                                   # A
+    qs, ks, qt, kt = draw(Hq, 128), draw(4, 128), draw(Hq, 128), draw(2, 128)  # B
+    qs8, ks8 = draw(Hq, 8), draw(4, 8)                                   # C (teacher as B)
+    lse_s = lse_stats(qs, ks, None, False)
+    lse_t = lse_stats(qt, kt, None, False)
+    lse_s8 = lse_stats(qs8, ks8, None, False)
+    P = T * T
+    stages = {
+        "A": (lambda: lse_stats(q, k, None, False), 2 * 128 * P,
+              f"lse_stats B={B} Hq={Hq} Hkv=4 T={T} D=128"),
+        "B": (lambda: kl_forward(qs, ks, lse_s, qt, kt, lse_t, None, False), 2 * (128 + 128) * P,
+              f"kl_forward B={B} Hq={Hq} Hkv_s=4 Hkv_t=2 T={T} Ds=Dt=128"),
+        "C": (lambda: kl_backward(qs8, ks8, lse_s8, qt, kt, lse_t, None, False), 2 * (8 + 128) * P + 4 * 8 * P,
+              f"kl_backward B={B} Hq={Hq} Hkv_s=4 Hkv_t=2 T={T} Ds=8 Dt=128"),
+    }
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for name, (fn, flops_bh, shape) in stages.items():
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        tflops = flops_bh * B * Hq / (ms * 1e-3) / 1e12
+        out[name] = {"shape": shape, "ms": ms, "tflops": tflops, "frac_fp16_peak": tflops / MI355X_BF16_DENSE_TFLOPS,
+                     "flops_per_call": flops_bh * B * Hq}
+        print(f"stage {name}: {ms:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    total = sum(v["ms"] for v in out.values())
+    dom = max(out, key=lambda k: out[k]["ms"])
+    print(json.dumps({
+        "metric": "stage entry points (A, B, C once each at the reference's gate shapes) relation rows/sec",
+        "value": B * Hq * T / (total * 1e-3), "unit": "relation-rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": total, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic (seeded N(0,1), fp16)",
+        "config": {"workload": "stage entry points at the reference gate shapes (fp16, non-causal, no mask)",
+                   "B": B, "Hq": Hq, "T": T},
+        "stages": out,
+        "roofline": {"bound": "mfma", "kernel": f"stage {dom}", "achieved": out[dom]["tflops"],
+                     "peak": MI355X_BF16_DENSE_TFLOPS, "unit": "TFLOP/s",
+                     "frac": out[dom]["tflops"] / MI355X_BF16_DENSE_TFLOPS, "traffic": None},
+    }))
+
+
 def run_rope(args):
     """The RoPE pair producer at the cfg4 shape (B=1, H=32, n=32768, d=128,
     bf16; teacher base 1e4, student linear factor 8): one pass reads the
@@ -583,11 +658,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (counter-scale calibration)")
-    ap.add_argument("--workload", default="relation", choices=("relation", "layers", "rope", "logits", "step"),
+    ap.add_argument("--workload", default="relation",
+                    choices=("relation", "layers", "rope", "logits", "step", "stages"),
                     help="relation: one self relation at --config (the headline); layers: the train.py "
                          "relation loss over --layers layers at cfg3 shapes, batched vs the per-call loop; "
                          "rope: the RoPE pair producer at the cfg4 shape; logits: the logits KL at the "
-                         "Llama-3-8B shape; step: the loss side of a cfg5 distillation step")
+                         "Llama-3-8B shape; step: the loss side of a cfg5 distillation step; stages: the "
+                         "stage entry points at the reference's gate shapes")
     ap.add_argument("--layers-step", type=int, default=32, help="layers of the step workload (cfg5: 32)")
     ap.add_argument("--layers", type=int, default=4)
     args = ap.parse_args()
@@ -607,6 +684,9 @@ def main():
         return
     if args.workload == "step":
         run_step(args)
+        return
+    if args.workload == "stages":
+        run_stages(args)
         return
 
     import torch

@@ -31,7 +31,8 @@ import csv
 import json
 import sys
 
-# kernel-name fragment -> timing-hook kernel id (include/linearard_amd.h)
+# kernel-name fragment -> kernel id (the timing hook's, include/linearard_amd.h,
+# for the throughput and logits kernels)
 KERNEL_NAMES = {
     "hot_fwdq_kernel": "forward_rowgrad",
     "hot_fwdq_batch_kernel": "forward_rowgrad",
@@ -41,6 +42,11 @@ KERNEL_NAMES = {
     "hot_bwd_kernel": "col_grad",
     "logits_kl_forward_kernel": "logits_forward",
     "logits_kl_grad_kernel": "logits_grad",
+    # the stage entry points' kernels (no timing-hook id: profile names only)
+    "row_kernel<0,": "stage_a_lse",
+    "row_kernel<1,": "stage_b_kl",
+    "row_kernel<2,": "stage_c_dq",
+    "col_kernel<": "stage_c_dk",
 }
 CALIBRATION_FRAGMENT = "neg_kernel"
 
@@ -109,7 +115,8 @@ def traffic(fetch_csv: str, write_csv: str, calib_mib: int, config: str) -> dict
 
 # MI355X: 8 XCDs, 32 CUs per XCD, 4 SIMDs per CU, 4 shader engines per XCD.
 XCDS, CUS, SIMDS, SES = 8, 256, 1024, 32
-KERNEL_ORDER = ("forward", "forward_rowgrad", "row_grad", "col_grad", "logits_forward", "logits_grad")
+KERNEL_ORDER = ("forward", "forward_rowgrad", "row_grad", "col_grad", "logits_forward", "logits_grad",
+                "stage_a_lse", "stage_b_kl", "stage_c_dq", "stage_c_dk")
 
 
 def counter_table(paths) -> dict:

@@ -31,6 +31,10 @@ def _check(got, ref, x, dtype):
     ("bf16", 2, 4, 300, 128, 8.0, False),
     ("f16", 1, 3, 77, 64, 4.0, True),
     ("bf16", 1, 2, 4096, 128, 8.0, False),  # large angles
+    # cfg4's rotations: positions up to 32767 (angles up to 32767 rad for the
+    # teacher), linear x8 student, base 1e4; in order and permuted
+    ("bf16", 1, 4, 32768, 128, 8.0, False),
+    ("bf16", 1, 2, 32768, 128, 8.0, True),
 ])
 def test_rope_pair_matches_oracle(gpu_available, dtype, B, H, T, D, factor, with_pos):
     from linearard_amd.rope import rope_inv_freq, rope_pair
