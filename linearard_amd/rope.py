@@ -21,6 +21,7 @@ functions.
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import json
 import math
@@ -31,7 +32,10 @@ from . import _lib
 
 __all__ = ["rope_inv_freq", "rope_pair", "rope_parameters"]
 
-_FREQ_CACHE = {}  # (dim, base, scaling, extras, device) -> (device tensor, attention scaling)
+# (dim, base, scaling, max_position_embeddings, length key, device) ->
+# (device tensor, attention scaling); least recently used entries go first
+_FREQ_CACHE = collections.OrderedDict()
+_FREQ_CACHE_SIZE = 32
 
 
 def _default_inv_freq(dim: int, base: float) -> torch.Tensor:
@@ -122,6 +126,37 @@ def rope_parameters(dim: int, base: float, rope_scaling=None, *, max_position_em
     raise NotImplementedError(f"rope_type {kind!r} is not built")
 
 
+def _length_key(rope_scaling, seq_len, max_position_embeddings):
+    """The part of a call's length that changes a rope type's table: dynamic
+    uses max(seq_len, max_position_embeddings), longrope only whether seq_len
+    exceeds original_max_position_embeddings, the other types nothing."""
+    scaling = dict(rope_scaling or {})
+    kind = scaling.get("rope_type", scaling.get("type", "default"))
+    if seq_len is None or kind not in ("dynamic", "longrope"):
+        return None
+    if kind == "dynamic":
+        max_pos = scaling.get("max_position_embeddings", max_position_embeddings)
+        return int(seq_len) if max_pos is None else max(int(seq_len), int(max_pos))
+    orig = scaling.get("original_max_position_embeddings")
+    return int(seq_len) if orig is None else bool(seq_len > orig)
+
+
+def _cached_parameters(dim, base, rope_scaling, max_position_embeddings, seq_len, device):
+    """rope_parameters with the table moved to `device`, from a bounded LRU cache."""
+    key = (dim, float(base), json.dumps(rope_scaling, sort_keys=True), max_position_embeddings,
+           _length_key(rope_scaling, seq_len, max_position_embeddings), str(device))
+    hit = _FREQ_CACHE.get(key)
+    if hit is not None:
+        _FREQ_CACHE.move_to_end(key)
+        return hit
+    inv, att = rope_parameters(dim, base, rope_scaling, max_position_embeddings=max_position_embeddings,
+                               seq_len=seq_len)
+    _FREQ_CACHE[key] = hit = (inv.to(device), float(att))
+    while len(_FREQ_CACHE) > _FREQ_CACHE_SIZE:
+        _FREQ_CACHE.popitem(last=False)
+    return hit
+
+
 def rope_inv_freq(dim: int, base: float, rope_scaling=None, device=None, **kw) -> torch.Tensor:
     """float32 [dim/2] inverse frequencies, computed like HF (on the CPU, then moved)."""
     inv, _ = rope_parameters(dim, base, rope_scaling, **kw)
@@ -154,16 +189,8 @@ def rope_pair(x: torch.Tensor, base: float, student_rope_scaling=None, position_
     if kind in ("dynamic", "longrope"):  # their tables depend on the call's longest position
         seq_len = T if position_ids is None else int(position_ids.max().item()) + 1
 
-    def params(b, scaling):
-        key = (D, float(b), json.dumps(scaling, sort_keys=True), max_position_embeddings, seq_len, str(dev))
-        if key not in _FREQ_CACHE:
-            inv, att = rope_parameters(D, b, scaling, max_position_embeddings=max_position_embeddings,
-                                       seq_len=seq_len)
-            _FREQ_CACHE[key] = (inv.to(dev), float(att))
-        return _FREQ_CACHE[key]
-
-    inv_t, att_t = params(base, None)
-    inv_s, att_s = params(sbase, student_rope_scaling)
+    inv_t, att_t = _cached_parameters(D, base, None, max_position_embeddings, seq_len, dev)
+    inv_s, att_s = _cached_parameters(D, sbase, student_rope_scaling, max_position_embeddings, seq_len, dev)
     out_t = torch.empty((B, H, T, D), device=dev, dtype=x.dtype)
     out_s = torch.empty((B, H, T, D), device=dev, dtype=x.dtype)
     pos_ptr, pos_sb = None, 0

@@ -144,3 +144,36 @@ def test_rope_oracle_attention_scaling_matches_torch():
     # a dropped scaling is caught
     plain = R.rope_apply(x, inv.numpy(), pos.numpy(), "bf16")
     assert (plain != ref).mean() > 0.5
+
+
+def test_frequency_cache_keys_on_what_changes_the_table_and_stays_bounded():
+    """rope_pair's table cache: a dynamic table is keyed on max(seq_len,
+    max_position_embeddings) and a longrope one on seq_len > original length,
+    so lengths that give the same table share one entry; the cache holds at
+    most _FREQ_CACHE_SIZE entries, and every entry equals rope_parameters."""
+    from linearard_amd import rope
+
+    rope._FREQ_CACHE.clear()
+    dyn = {"rope_type": "dynamic", "factor": 4.0}
+    for n in (10, 100, 256):  # <= max_position_embeddings: one table
+        inv, _ = rope._cached_parameters(64, 1e4, dyn, 256, n, "cpu")
+    assert len(rope._FREQ_CACHE) == 1
+    assert torch.equal(inv, rope.rope_parameters(64, 1e4, dyn, max_position_embeddings=256, seq_len=10)[0])
+    inv_long, _ = rope._cached_parameters(64, 1e4, dyn, 256, 1000, "cpu")
+    assert len(rope._FREQ_CACHE) == 2
+    assert torch.equal(inv_long, rope.rope_parameters(64, 1e4, dyn, max_position_embeddings=256, seq_len=1000)[0])
+    lr = {"rope_type": "longrope", "original_max_position_embeddings": 64, "factor": 4.0,
+          "short_factor": [1.0] * 32, "long_factor": [2.0] * 32}
+    for n in (3, 30, 64, 65, 500, 4000):
+        got, att = rope._cached_parameters(64, 1e4, lr, 256, n, "cpu")
+        want, att_w = rope.rope_parameters(64, 1e4, lr, max_position_embeddings=256, seq_len=n)
+        assert torch.equal(got, want) and att == att_w
+    assert len(rope._FREQ_CACHE) == 4  # short and long
+    for n in range(300, 300 + 3 * rope._FREQ_CACHE_SIZE):  # distinct dynamic lengths
+        rope._cached_parameters(64, 1e4, dyn, 256, n, "cpu")
+    assert len(rope._FREQ_CACHE) == rope._FREQ_CACHE_SIZE
+    other = {"rope_type": "linear", "factor": 8.0}
+    a = rope._cached_parameters(128, 1e4, other, None, 5, "cpu")
+    b = rope._cached_parameters(128, 1e4, other, None, 50000, "cpu")
+    assert a is b  # the length does not enter the key of a fixed table
+    rope._FREQ_CACHE.clear()

@@ -36,6 +36,56 @@ def _forward(L, xs, xt, mask, causal, a, noalloc):
     return loss, lse_s, lse_t
 
 
+def test_noalloc_first_call_captured_in_a_graph(gpu_available):
+    """The process's first noalloc call -- with its one-time lookup of this
+    device's scratch array -- made under HIP graph capture (this test runs
+    before the file's other noalloc calls); every replay on new input values
+    equals the workspace forward bitwise, and a warm eager call leaves the
+    device's free memory unchanged."""
+    L = _lib.lib()
+    B, H, T, D = 2, 4, 700, 128
+    a = 1 / math.sqrt(D)
+    g = torch.Generator(device="cuda").manual_seed(5)
+
+    def draw():
+        xt = torch.randn((B, H, T, D), device="cuda", generator=g)
+        return (xt + 0.3 * torch.randn(xt.shape, device="cuda", generator=g)).to(torch.bfloat16), \
+            xt.to(torch.bfloat16)
+
+    x_s, x_t = draw()  # static graph inputs and outputs
+    lse_s, lse_t = torch.empty((B, H, T), device="cuda"), torch.empty((B, H, T), device="cuda")
+    loss = torch.empty((), device="cuda")
+    d = [_lib.tensor4(x) for x in (x_s, x_s, x_t, x_t)]
+    md = _lib.mask_desc(None)
+
+    def call():
+        rc = L.lard_attn_kl_forward_noalloc(*[ctypes.byref(x) for x in d], ctypes.byref(md), 1, a, a,
+                                            lse_s.data_ptr(), lse_t.data_ptr(), loss.data_ptr(),
+                                            _lib.stream_of(x_s))
+        assert rc == 0, L.lard_last_error()
+
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(3):
+        s_new, t_new = draw()
+        x_s.copy_(s_new)
+        x_t.copy_(t_new)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (loss.clone(), lse_s.clone(), lse_t.clone())
+        want = _forward(L, s_new, t_new, None, True, a, noalloc=False)  # eager, between replays
+        for x, y in zip(got, want):
+            assert torch.equal(x, y), rep
+        assert got[0].item() > 0.0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    call()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+
+
 def test_noalloc_forward_equals_the_workspace_forward(gpu_available):
     L = _lib.lib()
     cases = [  # (dtype, B, H, T, D, mask ratio, causal): the second call is smaller
