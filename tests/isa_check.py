@@ -1,5 +1,10 @@
 """Static checks on the gfx950 assembly of the throughput kernels (CPU only).
 
+Three properties of the device code, checked on its assembly:
+
+* No writes through the scalar data cache anywhere (every kernel of every
+  source): device code writes memory through vector stores only.
+
 Two hazards the compiler cannot police for code it did not write itself:
 
 * M0.  The HBM->LDS copies (``lds_async16``, inline asm) write M0, which the
@@ -36,6 +41,11 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-featu
 RESULT_WAIT = 19
 # VALU write of a VGPR -> MFMA reads it: 2 wait states.
 OPERAND_WAIT = 2
+
+# Writes through the scalar data cache (scalar stores and atomics, the
+# cache's write-back and discard): none may appear in any kernel.
+SCALAR_WRITE = re.compile(r"^(s_store|s_buffer_store|s_scratch_store|s_atomic|s_buffer_atomic|s_dcache_wb"
+                          r"|s_dcache_discard)")
 
 IMPLICIT_M0 = re.compile(r"^(v_movrel|s_movrel|s_set_gpr_idx|s_sendmsg|ds_gws|v_interp|ds_\w*addtid|s_ttracedata)")
 
@@ -124,6 +134,11 @@ def check_m0(name: str, body) -> list:
             if not ok:
                 errs.append(f"{name}: {t!r} uses M0 outside the HBM->LDS copy sequence")
     return errs
+
+
+def check_no_scalar_writes(name: str, body) -> list:
+    return [f"{name}: {t!r} writes through the scalar data cache" for k, t in body
+            if k == "inst" and SCALAR_WRITE.match(_operands(t)[0])]
 
 
 def _successors(body, pos):

@@ -396,3 +396,48 @@ def test_single_valid_token_above_zero_non_causal(gpu_available):
     _check_lse(lse_t, ref_t, "single-token lse_t")
     got = lse_stats(x_s.detach(), x_s.detach(), m, False).cpu().numpy()  # stage A agrees
     _check_lse(got, ref_s, "single-token stage A")
+
+
+@pytest.mark.parametrize("self_rel", [1, 0])
+def test_keys_beyond_the_float16_range_take_a_scale(gpu_available, self_rel):
+    """bf16 inputs with a few entries of magnitude 2^15 to 2^17 (the rest
+    N(0, 256^2); scale 2^-19, inside the throughput kernels' range): the
+    float16 copies of the keys then take a power-of-two scale (the fix-up
+    pass after the conversion), for the student and the teacher, with the
+    large entries in k or, for q != k, only in q; against the float64 oracle."""
+    from linearard_amd import _lib
+    from linearard_amd.attention_KL import attn_kl_align
+
+    rng = np.random.default_rng(90 + self_rel)
+    B, Hq, T, D = 1, 2, 300, 64
+    Hkv = Hq if self_rel else 1
+    a = 2.0 ** -19
+
+    def draw(H, big):
+        x = rng.standard_normal((B, H, T, D)).astype(np.float32) * 256
+        if big:
+            idx = tuple(rng.integers(0, s, 6) for s in x.shape)
+            x[idx] = rng.choice([-1.0, 1.0], 6) * rng.uniform(2.0 ** 15, 2.0 ** 17, 6)
+        return O.round_to(x, "bf16")
+
+    if self_rel:
+        qs = ks = draw(Hq, True)
+        qt = kt = draw(Hq, True)
+    else:
+        qs, ks = draw(Hq, True), draw(Hkv, False)   # the student's large entries only in q
+        qt, kt = draw(Hq, False), draw(Hkv, True)   # the teacher's only in k
+    tqs = to_dev(qs, "bf16", requires_grad=True)
+    tks = tqs if self_rel else to_dev(ks, "bf16", requires_grad=True)
+    tqt = to_dev(qt, "bf16")
+    tkt = tqt if self_rel else to_dev(kt, "bf16")
+    L = _lib.lib()
+    d = [_lib.tensor4(x.detach()) for x in (tqs, tks, tqt, tkt)]
+    assert L.lard_attn_kl_path(*[ctypes.byref(x) for x in d], a, a) == 0  # the throughput kernels
+    loss = attn_kl_align(tqs, tks, tqt, tkt, causal=True, sm_scale_s=a, sm_scale_t=a)
+    loss.backward()
+    rl, rdq, rdk, _, _ = O.attn_kl_align(qs, ks, qt, kt, None, True, a, a, self_relation=bool(self_rel))
+    cid = f"f16-key-scale-self{self_rel}"
+    check_loss(loss.item(), rl, cid)
+    check_grad(tqs.grad.float().cpu().numpy(), rdq, cid, "dX" if self_rel else "dq")
+    if not self_rel:
+        check_grad(tks.grad.float().cpu().numpy(), rdk, cid, "dk")

@@ -1,5 +1,6 @@
 """Static checks of the compiled gfx950 kernels (CPU; hipcc cross-compiles).
 
+* No kernel of any source writes through the scalar data cache.
 * The HBM->LDS copy sequence is the only user of M0 in the throughput
   kernels (hot.hip, hot_fwdq.hip): the copies write M0 from inline asm while
   the compiler reserves it.
@@ -26,10 +27,31 @@ def asm_dir(tmp_path_factory):
     return str(tmp_path_factory.mktemp("isa"))
 
 
+_ASM = {}
+
+
+def _kernels(src, asm_dir):
+    """Kernels of one source's gfx950 assembly (compiled once per session)."""
+    if src not in _ASM:
+        _ASM[src] = C.kernels(C.device_asm(os.path.join(CSRC, src), asm_dir))
+    return _ASM[src]
+
+
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+@needs_hipcc
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_writes_through_the_scalar_cache(asm_dir, src):
+    ks = _kernels(src, asm_dir)
+    errs = [e for name, body in ks.items() for e in C.check_no_scalar_writes(name, body)]
+    assert not errs, "\n".join(errs[:20])
+
+
 @needs_hipcc
 @pytest.mark.parametrize("src", ["hot.hip", "hot_fwdq.hip"])
 def test_m0_only_in_the_copy_sequence(asm_dir, src):
-    ks = C.kernels(C.device_asm(os.path.join(CSRC, src), asm_dir))
+    ks = _kernels(src, asm_dir)
     assert ks, "no kernels found"
     errs = [e for name, body in ks.items() for e in C.check_m0(name, body)]
     assert not errs, "\n".join(errs[:20])
@@ -39,7 +61,7 @@ def test_m0_only_in_the_copy_sequence(asm_dir, src):
 
 @needs_hipcc
 def test_fused_forward_mfma_wait_states(asm_dir):
-    ks = C.kernels(C.device_asm(os.path.join(CSRC, "hot_fwdq.hip"), asm_dir))
+    ks = _kernels("hot_fwdq.hip", asm_dir)
     fused = {n: b for n, b in ks.items() if "hot_fwdq" in n}
     assert len(fused) == 16, sorted(fused)  # {16, 32, 64, 128} x {bf16, f16} x {single, batch}
     errs = [e for name, body in fused.items() for e in C.check_mfma_hazards(name, body)]
@@ -80,6 +102,10 @@ def test_checker_catches_planted_hazards():
     acc = "v_mfma_f32_32x32x16_bf16 a[0:15], v[16:19], v[20:23], a[0:15]"
     assert C.check_mfma_hazards("k", _body([acc, "s_cbranch_scc1 .LBB0_2", "s_nop 7", "s_nop 7", "s_nop 7",
                                             ".LBB0_2:", "v_accvgpr_read_b32 v1, a4", "s_endpgm"]))
+    # a scalar store and a scalar atomic
+    assert C.check_no_scalar_writes("k", _body(["s_store_dword s4, s[0:1], 0x0"]))
+    assert C.check_no_scalar_writes("k", _body(["s_atomic_add s4, s[0:1], 0x0"]))
+    assert not C.check_no_scalar_writes("k", _body(["s_load_dword s4, s[0:1], 0x0", "global_store_dword v0, v1, off"]))
     # M0 outside the copy sequence, and an implicit reader
     assert C.check_m0("k", _body(["s_mov_b32 m0, s4", "ds_read_b32 v0, v1"]))
     assert C.check_m0("k", _body(["s_sendmsg sendmsg(MSG_INTERRUPT)"]))
