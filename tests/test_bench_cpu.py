@@ -44,7 +44,7 @@ def test_cfg5_step_work_is_633_tflop():
 def test_committed_traffic_summary_is_readable():
     s = bench.traffic_summary("cfg4")
     assert s is not None
-    for k in ("forward", "row_grad", "col_grad"):
+    for k in ("forward_rowgrad", "col_grad"):  # the autograd path's two kernels
         assert s["bytes_per_launch"][k] > 0
         # read + write bytes add up to the total per launch
         assert abs(s["read_bytes"][k] + s["write_bytes"][k] - s["bytes_per_launch"][k]) <= 1e-6 * s["bytes_per_launch"][k]
