@@ -14,11 +14,12 @@ HBM, and a CPU baseline: the oracle's linear-memory float32 restatement run
 on this host for one (b, h) relation, scaled to the same unit.
 
 Roofline: the library's timing hook (lard_timing_*) brackets each launch of
-its three kernels with HIP events on the launch stream during the timed
-steps.  Each kernel is credited 4*d*P algorithmic flops per (b, h): the
-forward owns S_s and S_t (2 GEMMs), each backward kernel owns one of the two
-gradient products (D.K_s, D^T.Q_s) plus half of the S_s, S_t recompute.  The
-dominant kernel is the one with the longest average launch.  `traffic` (HBM
+its kernels with HIP events on the launch stream during a second pass of
+the same steps.  The autograd path runs two kernels, each credited 6*d*P
+algorithmic flops per (b, h): the fused forward owns S_s, S_t (2 GEMMs) and
+the row-side gradient product, the column kernel the recompute of S_s, S_t
+and D^T.Q_s (12*d*P in all).  The dominant kernel is the one with the
+longest average launch.  `traffic` (HBM
 bytes per launch of that kernel) comes from the counter summary
 profiles/traffic_<config>.json when present (rocprofv3 FETCH_SIZE and
 WRITE_SIZE runs of this script with --copy-calibration, scaled by a plain
