@@ -441,3 +441,42 @@ def test_keys_beyond_the_float16_range_take_a_scale(gpu_available, self_rel):
     check_grad(tqs.grad.float().cpu().numpy(), rdq, cid, "dX" if self_rel else "dq")
     if not self_rel:
         check_grad(tks.grad.float().cpu().numpy(), rdk, cid, "dk")
+
+
+@pytest.mark.parametrize("case", ["self", "gqa", "batched"])
+def test_second_backward_through_the_same_graph(gpu_available, case):
+    """retain_graph: the first backward adds the column side to the row side
+    the forward formed; the second finds that buffer consumed and runs the
+    full backward.  Both gradients against the float64 oracle."""
+    from linearard_amd.attention_KL import attn_kl_align, attn_kl_align_batched
+
+    rng = np.random.default_rng(61)
+    B, Hq, T, D = 2, 4, 300, 128
+    Hkv = 2 if case == "gqa" else Hq
+    qt = randn(rng, (B, Hq, T, D), "bf16")
+    qs = O.round_to(qt + 0.3 * rng.standard_normal(qt.shape).astype(np.float32), "bf16")
+    mask = make_mask(rng, B, T, 0.2)
+    m = mask_to_dev(mask)
+    if case == "gqa":
+        kt = randn(rng, (B, Hkv, T, D), "bf16")
+        ks = O.round_to(kt + 0.3 * rng.standard_normal(kt.shape).astype(np.float32), "bf16")
+        x_q, x_k = to_dev(qs, "bf16", True), to_dev(ks, "bf16", True)
+        y_q, y_k = to_dev(qt, "bf16"), to_dev(kt, "bf16")
+        loss = attn_kl_align(x_q, x_k, y_q, y_k, attn_mask=m, causal=True)
+        inputs = [x_q, x_k]
+        rl, rdq, rdk, _, _ = O.attn_kl_align(qs, ks, qt, kt, mask, True)
+        refs = [("dq", rdq), ("dk", rdk)]
+    else:
+        x, y = to_dev(qs, "bf16", True), to_dev(qt, "bf16")
+        if case == "self":
+            loss = attn_kl_align(x, x, y, y, attn_mask=m, causal=True)
+        else:
+            loss = attn_kl_align_batched([x], [y], attn_mask=m, causal=True)
+        inputs = [x]
+        rl, rdx, _, _, _ = O.attn_kl_align(qs, qs, qt, qt, mask, True, self_relation=True)
+        refs = [("dX", rdx)]
+    check_loss(loss.item(), rl, f"second-backward-{case}")
+    for rep in ("first", "second"):
+        grads = torch.autograd.grad(loss, inputs, retain_graph=True)
+        for (name, ref), g in zip(refs, grads):
+            check_grad(g.float().cpu().numpy(), ref, f"second-backward-{case}-{rep}", name)
