@@ -78,10 +78,14 @@ def pre_rope(g, B, H, n, d, *, outliers=0, head_std=False, t_channels=0):
     return v
 
 
-def config_relations(name, seed=0):
-    """Inputs of a BASELINE configuration on the GPU (
-    drawn from one seeded CUDA generator in a fixed order):
+def config_relations(name, seed=0, device_rng=False):
+    """Inputs of a BASELINE configuration on the GPU:
     {"q": (x_s, x_t), "k": ..., "v": ..., "B": B, "n": n, "d": d, "mask": m}.
+
+    Drawn on the CPU from torch.Generator().manual_seed(seed) in a fixed
+    order, then moved to the GPU (so the inputs can be regenerated without
+    a GPU); device_rng=True draws from a seeded CUDA generator instead (other
+    values; for callers that need many layers quickly).
 
     cfg1  B=1, H=32, n=1024, d=128, float32: x_t ~ N(0,1), x_s = x_t + 0.1 N(0,1)
           (Q/Q only).
@@ -102,26 +106,30 @@ def config_relations(name, seed=0):
 
     from linearard_amd.rope import rope_pair
 
-    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev if device_rng else "cpu").manual_seed(seed)
     bf = torch.bfloat16
 
+    def gpu(x, dtype=None):
+        return x.to(device=dev, dtype=dtype)
+
     def rotated(v, base, scaling=None, student_base=None):
-        return rope_pair(v.to(bf), base, scaling, student_base=student_base)
+        return rope_pair(gpu(v, bf), base, scaling, student_base=student_base)
 
     if name == "cfg1":
-        xt = torch.randn((1, 32, 1024, 128), generator=g, device="cuda")
-        xs = xt + 0.1 * torch.randn(xt.shape, generator=g, device="cuda")
-        return {"q": (xs, xt), "B": 1, "n": 1024, "d": 128, "mask": None}
+        xt = torch.randn((1, 32, 1024, 128), generator=g, device=g.device)
+        xs = xt + 0.1 * torch.randn(xt.shape, generator=g, device=g.device)
+        return {"q": (gpu(xs), gpu(xt)), "B": 1, "n": 1024, "d": 128, "mask": None}
     if name == "cfg2":
         lin8 = {"rope_type": "linear", "factor": 8.0}
         out = {k: rotated(pre_rope(g, 1, 32, 4096, 128, outliers=4), 1e4, lin8) for k in ("q", "k")}
-        v = pre_rope(g, 1, 32, 4096, 128, outliers=4).to(bf)
+        v = gpu(pre_rope(g, 1, 32, 4096, 128, outliers=4), bf)
         out.update(v=(v, v), B=1, n=4096, d=128, mask=None)
         return out
     if name == "cfg3":
         out = {k: rotated(pre_rope(g, 1, H, 8192, 128, head_std=True), 5e5, None, 5e5 * 8.0)
                for k, H in (("q", 32), ("k", 8))}
-        v = pre_rope(g, 1, 8, 8192, 128, head_std=True).to(bf)
+        v = gpu(pre_rope(g, 1, 8, 8192, 128, head_std=True), bf)
         out.update(v=(v, v), B=1, n=8192, d=128, mask=None)
         return out
     if name in ("cfg4", "small"):
@@ -132,9 +140,9 @@ def config_relations(name, seed=0):
         lin4 = {"rope_type": "linear", "factor": 4.0}
         out = {k: rotated(pre_rope(g, 2, H, 16384, 128, t_channels=8), 1e4, lin4) for k, H in (("q", 32), ("k", 8))}
         vt = pre_rope(g, 2, 8, 16384, 128, t_channels=8)
-        vs = vt + 0.1 * torch.randn(vt.shape, generator=g, device="cuda")
-        out.update(v=(vs.to(bf), vt.to(bf)), B=2, n=16384, d=128,
-                   mask=torch.ones((2, 16384), dtype=torch.int64, device="cuda"))
+        vs = vt + 0.1 * torch.randn(vt.shape, generator=g, device=g.device)
+        out.update(v=(gpu(vs, bf), gpu(vt, bf)), B=2, n=16384, d=128,
+                   mask=torch.ones((2, 16384), dtype=torch.int64, device=dev))
         return out
     raise ValueError(f"unknown configuration {name!r}")
 
@@ -638,8 +646,9 @@ def run_step(args):
         "value": rel_tokens / (ms * 1e-3), "unit": "relation-tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "wall_ms_per_step": wall, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded Gaussian activations with 8 Student-t(3) channels; RoPE teacher at p, "
-                "student at p/4; logits teacher + noise)",
+        "data": "synthetic (Gaussian activations with 8 Student-t(3) channels from a seeded device generator: "
+                "32 layers from the CPU generator would take minutes; RoPE teacher at p, student at p/4; "
+                "logits teacher + noise)",
         "config": {"workload": f"cfg5 step: {Lyr} layers x (Q/Q {Hq} heads, K/K {Hkv}, V/V {Hkv}), B={B}, n={n}, "
                                f"d={d}, causal, all-ones mask; logits [{B}, {Kkeep}, {vocab}], lam_A=1, lam_L=0",
                    "layers": Lyr, "B": B, "n": n, "d": d, "Hq": Hq, "Hkv": Hkv},
@@ -805,7 +814,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": f"synthetic ({data[args.config]}; RoPE by the pair producer)",
+        "data": f"synthetic ({data[args.config]}; drawn on the CPU from torch.Generator().manual_seed(0), moved "
+                f"to the GPU; RoPE by the pair producer)",
         "config": {"workload": f"{args.config}: self-relation Q/Q KL fwd+bwd, B={B}, H={H}, n={n}, d={d}, causal",
                    "B": B, "H": H, "n": n, "d": d, "causal": True},
         "tflops": flops / (ms * 1e-3) / 1e12,

@@ -142,7 +142,7 @@ def test_distillation_step_at_the_cfg5_launch_shape(gpu_available):
 
     L, B, n, Hq = 8, 2, 16384, 32
     a = 1 / math.sqrt(128)
-    rels = [bench.config_relations("cfg5", seed=500 + l) for l in range(L)]
+    rels = [bench.config_relations("cfg5", seed=500 + l, device_rng=True) for l in range(L)]
     mask = rels[0]["mask"]
     s = {k: [r[k][0].detach().clone().requires_grad_(True) for r in rels] for k in "qkv"}
     t = {k: [r[k][1] for r in rels] for k in "qkv"}
