@@ -22,7 +22,8 @@ Two hazards the compiler cannot police for code it did not write itself:
       for ``RESULT_WAIT`` wait states, except by the next MFMA of the same
       accumulation chain (source C == destination, exactly);
     - no VALU instruction writes an MFMA source register in the
-      ``OPERAND_WAIT`` wait states before it.
+      ``OPERAND_WAIT`` wait states before it, on any path into it (across
+      branches and labels).
 
 Used by ``tests/test_isa.py``; nothing in the product imports it.
 """
@@ -196,8 +197,46 @@ def _scan_result(body, start, regs, chain_dst):
     return worst
 
 
+def _predecessors(body):
+    """position -> positions control may come from directly (fall-through
+    from the previous instruction unless that ends the path, and every branch
+    whose target is that label)."""
+    preds = {i: [] for i in range(len(body))}
+    for j, (kind, t) in enumerate(body):
+        succ = _successors(body, j) if kind == "inst" else [j + 1]
+        for s2 in succ:
+            if s2 < len(body):
+                preds[s2].append(j)
+    return preds
+
+
+def _scan_operand_writes(body, preds, i, srcs):
+    """Wait states between VALU writes of srcs and the MFMA at i, on every
+    path into it, for writes closer than OPERAND_WAIT: [(position, distance)]."""
+    hits = []
+    stack = [(p, 0) for p in preds[i]]
+    seen = set()
+    while stack:
+        pos, ws = stack.pop()
+        if ws >= OPERAND_WAIT or (pos, ws) in seen:
+            continue
+        seen.add((pos, ws))
+        kind, t = body[pos]
+        step = 0
+        if kind == "inst":
+            op, ops = _operands(t)
+            if op.startswith("v_") and not op.startswith("v_mfma") and ops and _regs(ops[0]) & srcs:
+                hits.append((pos, ws))
+                continue
+            step = _wait_states(t)
+        for p in preds[pos]:
+            stack.append((p, ws + step))
+    return hits
+
+
 def check_mfma_hazards(name: str, body) -> list:
     errs = []
+    preds = _predecessors(body)
     for i, (kind, t) in enumerate(body):
         if kind != "inst" or not t.startswith("v_mfma"):
             continue
@@ -206,20 +245,10 @@ def check_mfma_hazards(name: str, body) -> list:
         d = _scan_result(body, i, dst, ops[0])
         if d is not None:
             errs.append(f"{name}: result of {t!r} (#{i}) is touched {d} wait states later (< {RESULT_WAIT})")
-        # VALU writes of the sources within OPERAND_WAIT before (same block)
+        # VALU writes of the sources within OPERAND_WAIT before, on every path
         srcs = set()
         for o in ops[1:4]:
             srcs |= _regs(o)
-        ws = 0
-        j = i - 1
-        while j >= 0 and ws < OPERAND_WAIT:
-            k2, t2 = body[j]
-            if k2 == "label":
-                errs.append(f"{name}: {t!r} (#{i}) starts a block; its operand writes cannot be checked")
-                break
-            op2, ops2 = _operands(t2)
-            if op2.startswith("v_") and not op2.startswith("v_mfma") and ops2 and _regs(ops2[0]) & srcs:
-                errs.append(f"{name}: {t2!r} writes an operand of {t!r} {ws} wait states before it")
-            ws += _wait_states(t2)
-            j -= 1
+        for pos, ws in _scan_operand_writes(body, preds, i, srcs):
+            errs.append(f"{name}: {body[pos][1]!r} writes an operand of {t!r} {ws} wait states before it")
     return errs

@@ -98,6 +98,15 @@ def test_checker_catches_planted_hazards():
                                             "s_nop 3", "s_endpgm"]))
     assert not C.check_mfma_hazards("k", _body(["v_mov_b32_e32 v17, 0", "s_nop 1", mfma, "s_nop 7", "s_nop 7",
                                                 "s_nop 3", "s_endpgm"]))
+    # an operand written in a predecessor block: by the branch's block and by fall-through
+    assert C.check_mfma_hazards("k", _body(["v_mov_b32_e32 v17, 0", "s_cbranch_scc1 .LBB0_1", "s_nop 7",
+                                            ".LBB0_1:", mfma, "s_nop 7", "s_nop 7", "s_nop 3", "s_endpgm"]))
+    assert C.check_mfma_hazards("k", _body(["s_cbranch_scc1 .LBB0_1", "v_mov_b32_e32 v17, 0",
+                                            ".LBB0_1:", mfma, "s_nop 7", "s_nop 7", "s_nop 3", "s_endpgm"]))
+    # ... and far enough on both paths
+    assert not C.check_mfma_hazards("k", _body(["v_mov_b32_e32 v17, 0", "s_nop 0", "s_cbranch_scc1 .LBB0_1",
+                                                "s_nop 1", ".LBB0_1:", mfma, "s_nop 7", "s_nop 7", "s_nop 3",
+                                                "s_endpgm"]))
     # AGPR accumulators, read back too early along a branch target
     acc = "v_mfma_f32_32x32x16_bf16 a[0:15], v[16:19], v[20:23], a[0:15]"
     assert C.check_mfma_hazards("k", _body([acc, "s_cbranch_scc1 .LBB0_2", "s_nop 7", "s_nop 7", "s_nop 7",
