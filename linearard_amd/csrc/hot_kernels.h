@@ -950,6 +950,7 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
   // per query row of the tile: -lse*log2(e) of student [0, 64) and teacher [64, 128)
   __shared__ __attribute__((aligned(16))) float lnl[kBufs][2 * kTile];
   static_assert(2 * kTile * sizeof(float) == kWaves * 64, "one 64-byte row-data copy per wave");
+  static_assert(kWaves == 8 && 2 * kTile * sizeof(float) == 4 * 128, "refills: 4 waves, 128 bytes of row data each");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -992,6 +993,13 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
   RowCopier<DP> cp_s, cp_t;
   cp_s.init((int)a.s.q_st, a.s.dim, w, lane);
   cp_t.init((int)a.t.q_st, a.t.dim, w, lane);
+  // Ring refills come from waves 0-3 alone (wave & 3 is the SIMD): with two
+  // waves per SIMD the older one wins issue arbitration and reaches each
+  // barrier first, so its copy-issue stall overlaps the younger wave's compute
+  // instead of stalling both waves of the SIMD.
+  RowCopier<DP, 4> cq_s, cq_t;
+  cq_s.init((int)a.s.q_st, a.s.dim, w & 3, lane);
+  cq_t.init((int)a.t.q_st, a.t.dim, w & 3, lane);
   TrOffsets<DP> tro;
   tro.init(lane);
   int loaded_ht = -1;
@@ -1020,6 +1028,16 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
       cp_s.issue(lq[buf][0], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
       cp_t.issue(lq[buf][1], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
       issue_small(&lnl[buf][16 * w], nl_src + i0, lane);
+    };
+    // the same tile from waves 0-3 only; wave q = w & 3 copies 32 normalisers:
+    // student rows 32q.. (q < 2), teacher rows 32(q-2).. (q >= 2)
+    const float* nl_src4 = ((w & 3) < 2 ? f.nl_s : f.nl_t) + bh * f.Tp + 32 * (w & 1);
+    auto issue_tile4 = [&](int it) {
+      const int buf = it % kBufs;
+      const int i0 = tile_of(it) * kTile;
+      cq_s.issue(lq[buf][0], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w & 3, lane);
+      cq_t.issue(lq[buf][1], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w & 3, lane);
+      if (lane < 8) lds_async16(nl_src4 + i0, 16u * lane, &lnl[buf][32 * (w & 3)]);
     };
     auto compute_tile = [&](int it) {
       const int buf = it % kBufs;
@@ -1081,8 +1099,10 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
       if (p + 2 < ntiles) {
         wait_vmcnt<0>();
         __syncthreads();
-        if (p + 4 < ntiles) issue_tile(p + 4);
-        if (p + 5 < ntiles) issue_tile(p + 5);
+        if (w < 4) {
+          if (p + 4 < ntiles) issue_tile4(p + 4);
+          if (p + 5 < ntiles) issue_tile4(p + 5);
+        }
       }
     }
     __syncthreads();  // every wave is done with the ring before the next head refills it
