@@ -2,12 +2,14 @@
 (integration.py:6-73) against the float64 oracle (oracle.attn_kl).
 
 The cases put T at and around the kernels' tile sizes (64-key tiles,
-256-row workgroups: 63, 65, 255, 256, 257, 511), at T = 1, and mix:
+256-row workgroups: 63, 65, 255, 256, 257, 511), at T = 1, past four query
+tiles per column block at every padded head dim (333-700), and mix:
 - GQA ratios, for the self relation and for the general q != k relation;
 - padding masks, including one kept token and none;
 - causal and non-causal;
 - fp16 and bf16;
-- D = 64, 128 (the throughput kernels) and D = 256 (the fused path);
+- D = 8, 16, 32, 64, 128 (the throughput kernels, head dims padded to 16,
+  32, 64, 128) and D = 256 (the fused path);
 - unequal student and teacher scales.
 """
 
@@ -17,6 +19,8 @@ import numpy as np
 import pytest
 import torch
 
+from linearard_amd import _lib
+from linearard_amd.attention_KL.integration import kernel_path
 from oracle import attn_kl as O
 from tests._inputs import make_mask, mask_to_dev, randn, to_dev
 from tests._tolerance import check_grad, check_loss
@@ -38,6 +42,14 @@ CASES = [
     ("bf16", 1, 2, 2, 300, 256, None, True, 1.0, True),
     ("bf16", 2, 2, 2, 129, 128, 1.0, True, 1.0, True),  # only token 0 of each sequence kept
     ("bf16", 2, 2, 2, 70, 128, "none", True, 1.0, True),  # no token kept
+    # five or more 64-row query tiles per column block, so the column
+    # kernel's ring is refilled inside its loop, at every padded head dim
+    # (16, 32, 64): odd and even tile counts, a partial last tile
+    ("f16", 1, 2, 2, 400, 8, None, True, 1.0, True),
+    ("bf16", 1, 2, 1, 400, 16, 0.3, False, 1.0, False),
+    ("bf16", 1, 2, 2, 450, 32, None, True, 1.2, True),
+    ("f16", 2, 2, 2, 333, 64, 0.4, True, 1.0, True),
+    ("bf16", 1, 4, 2, 700, 64, None, False, 1.0, False),
 ]
 
 
@@ -50,6 +62,11 @@ def test_autograd_sweep(gpu_available, case):
     rng = np.random.default_rng(1000 + 7 * T + Hq + D)
     a_s = 1 / math.sqrt(D)
     a_t = a_s * sr
+    if T > 256 and D <= 128:
+        # the throughput kernels, with the column kernel's in-loop refills
+        x = torch.empty((B, Hq, T, D), device="cuda", dtype=torch.bfloat16 if dtype == "bf16" else torch.float16)
+        d = [_lib.tensor4(x)] * 4
+        assert kernel_path(d, a_s, a_t)[0] == "throughput", kernel_path(d, a_s, a_t)
     if ratio == "none":
         mask = np.zeros((B, T), dtype=np.int32)
     else:
