@@ -307,6 +307,47 @@ __device__ __forceinline__ void mask_block_q(f32x16& ss, f32x16& st, unsigned bi
   }
 }
 
+
+// LDS byte address of a shared-memory pointer, and loads at such addresses.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+__device__ __forceinline__ u16x8 lds_u16x8(unsigned a) {
+  return *(__attribute__((address_space(3))) const u16x8*)(uintptr_t)a;
+}
+// Transposing operand reads (TrOffsets' pattern) with the swizzle's per-lane
+// offsets in XOR form.  The swizzle XORs the chunk index inside a row, so in
+// a 256-byte aligned tile the offset of dim block db is the lane's db = 0
+// offset with address bits 6-7 flipped by db (one base per 8-row half: for
+// D = 128 the two halves swizzle differently), while the 16-row groups and
+// sub-blocks add.  Two registers per lane instead of eight, and the constant
+// parts fold into the reads' offset field; with the offsets in VGPRs the
+// compiler no longer parks them in AGPRs and reads them back every step.
+template <int DP>
+struct TrXor {
+  unsigned base[2];  // bytes
+  __device__ __forceinline__ void init(int lane) {
+    const int g = lane >> 4, u = lane & 15;
+    int dim = 16 * (g & 1) + 4 * (u & 3);
+    if (DP < 32) dim &= DP - 1;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = 8 * r + 4 * (g >> 1) + (u >> 2);
+      base[r] = 2u * ((unsigned)row_chunk_off<DP>(row, dim >> 3) + (dim & 7));
+    }
+  }
+  __device__ __forceinline__ u16x8 read(unsigned tile, int sb, int m, int db) const {
+    s16x4 v[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const unsigned a = ((tile + base[r]) ^ (unsigned)(db << 6)) + (unsigned)((32 * sb + 16 * m) * DP * 2);
+      v[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)a);
+    }
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 both = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(u16x8, both);
+  }
+};
 // Lazy-maximum bound of the fused kernel: every exponential stays below it,
 // so the float16 operands (largest finite 65504) never overflow.
 constexpr float kLazySumQ = 32768.f;  // 2^15
@@ -323,7 +364,10 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   static_assert(PPK * KS == NP, "output products must spread evenly over the score k-steps");
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
   constexpr int kBufs = 4;
-  __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
+  // [buffer][student, teacher]; 256-byte aligned for the XOR-form operand
+  // addresses (g1b, TrXor)
+  __shared__ __attribute__((aligned(256))) u16 lk[kBufs][2][kTile * DP];
+  static_assert((32 * DP * 2) % 256 == 0, "tiles and sub-blocks start 256-byte aligned");
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWavesQ][kTile];
 
   const int tid = threadIdx.x;
@@ -401,10 +445,10 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     cp_t.issue(lk[buf][1], kt_base, (int)f.k16t_st, j0, T, a.t.dim, w, lane);
     issue_small(ltok[buf][w], tok + j0, lane);
   };
-  unsigned g1off[KS];  // this lane's row chunks of a sub-block: row l32, chunk 2kk + half
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) g1off[kk] = (unsigned)row_chunk_off<DP>(l32, 2 * kk + half);
-  TrOffsets<DP> tro;
+  // this lane's row chunk of a sub-block, bytes: row l32, chunk half; chunk
+  // 2kk + half is at (tile + g1b) ^ (kk << 5) (the swizzle XORs the chunk)
+  const unsigned g1b = 2u * (unsigned)row_chunk_off<DP>(l32, half);
+  TrXor<DP> tro;
   tro.init(lane);
 
   f32x16 o_s[NDB], o_t[NDB];  // O^T: lane l holds row i = l%32, dims 32db + 8(r/4) + 4half + r%4
@@ -449,12 +493,13 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     constexpr int PD = 1;  // score operands read PD k-steps ahead
     constexpr int PA = 1;  // output-product A operands read PA pairs ahead
     u16x8 os[KS], ot[KS], oa[NP];
+    const unsigned ad1 = lds_addr(t1) + g1b, ad2 = lds_addr(t2);
     auto load1 = [&](int kk) {
-      const u16* p = t1 + g1off[kk];
-      os[kk] = *reinterpret_cast<const u16x8*>(p);
-      ot[kk] = *reinterpret_cast<const u16x8*>(p + kTile * DP);
+      const unsigned p = ad1 ^ (unsigned)(kk << 5);
+      os[kk] = lds_u16x8(p);
+      ot[kk] = lds_u16x8(p + kTile * DP * 2);
     };
-    auto load2 = [&](int j) { oa[j] = tro.read(t2, sb2, j / NDB, j % NDB); };
+    auto load2 = [&](int j) { oa[j] = tro.read(ad2, sb2, j / NDB, j % NDB); };
     static_assert(PD == 1 && PA == 1, "the carried operands are the first k-step's");
     if constexpr (PRE1_IN) {
       os[0] = pre_os;
@@ -487,11 +532,11 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
         if (j + PA < NP) load2(j + PA);
       }
       if (kk == KS - 1) {  // the next step's first operands
-        pre_oa = tro.read(lk[buf_of(k)][0], k & 1, 0, 0);
+        pre_oa = tro.read(lds_addr(lk[buf_of(k)][0]), k & 1, 0, 0);
         if constexpr (PRE1_OUT) {
-          const u16* p = lk[buf_of(k + 2)][0] + 32 * (k & 1) * DP + g1off[0];  // sub-block k+2 has k's half
-          pre_os = *reinterpret_cast<const u16x8*>(p);
-          pre_ot = *reinterpret_cast<const u16x8*>(p + kTile * DP);
+          const unsigned p = lds_addr(lk[buf_of(k + 2)][0] + 32 * (k & 1) * DP) + g1b;  // sub-block k+2 has k's half
+          pre_os = lds_u16x8(p);
+          pre_ot = lds_u16x8(p + kTile * DP * 2);
         }
       }
       float xt[NPAIR][2], xs[NPAIR][2], dd[NPAIR][2];
@@ -595,10 +640,10 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   A.tm = __ballot(ltok[0][w][lane] != 0);
   sub_scores_q<DP, BF>(lk[0][0], 0, l32, half, fq_s, fq_t, A.s, A.t);
   {  // what step 0 would have carried: scores of sub-block 1, products of "sub-block -1" (zero operands)
-    const u16* p = lk[0][0] + 32 * DP + g1off[0];
-    pre_os = *reinterpret_cast<const u16x8*>(p);
-    pre_ot = *reinterpret_cast<const u16x8*>(p + kTile * DP);
-    pre_oa = tro.read(lk[0][0], 0, 0, 0);
+    const unsigned p = lds_addr(lk[0][0] + 32 * DP) + g1b;
+    pre_os = lds_u16x8(p);
+    pre_ot = lds_u16x8(p + kTile * DP * 2);
+    pre_oa = tro.read(lds_addr(lk[0][0]), 0, 0, 0);
   }
   for (int k = 0; k < nsub; k += 2) {
     step(A, k, B, k + 1, std::true_type{}, std::false_type{});
@@ -622,7 +667,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     const u16* t2 = lk[buf_of(k2)][0];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-      const u16x8 op = tro.read(t2, k2 & 1, j / NDB, j % NDB);
+      const u16x8 op = tro.read(lds_addr(t2), k2 & 1, j / NDB, j % NDB);
       mfma_oacc<false>(j % NDB, o_s[j % NDB], op, pop_s[j / NDB]);
       mfma_oacc<false>(NDB + j % NDB, o_t[j % NDB], op, pop_t[j / NDB]);
     }
