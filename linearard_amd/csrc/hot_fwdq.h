@@ -308,10 +308,7 @@ __device__ __forceinline__ void mask_block_q(f32x16& ss, f32x16& st, unsigned bi
 }
 
 
-// LDS byte address of a shared-memory pointer, and loads at such addresses.
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
+// A 16-byte LDS load at a byte address.
 __device__ __forceinline__ u16x8 lds_u16x8(unsigned a) {
   return *(__attribute__((address_space(3))) const u16x8*)(uintptr_t)a;
 }
@@ -441,9 +438,9 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   auto issue_tile = [&](int it) {
     const int buf = it % kBufs;
     const int j0 = tile_of(it) * kTile;
-    cp_s.issue(lk[buf][0], ks_base, (int)f.k16_st, j0, T, a.s.dim, w, lane);
-    cp_t.issue(lk[buf][1], kt_base, (int)f.k16t_st, j0, T, a.t.dim, w, lane);
-    issue_small(ltok[buf][w], tok + j0, lane);
+    cp_s.issue(lds_addr(lk[buf][0]), ks_base, (int)f.k16_st, j0, T, a.s.dim, w, lane);
+    cp_t.issue(lds_addr(lk[buf][1]), kt_base, (int)f.k16t_st, j0, T, a.t.dim, w, lane);
+    issue_small(lds_addr(ltok[buf][w]), tok + j0, lane);
   };
   // this lane's row chunk of a sub-block, bytes: row l32, chunk half; chunk
   // 2kk + half is at (tile + g1b) ^ (kk << 5) (the swizzle XORs the chunk)

@@ -64,9 +64,19 @@ struct HotArgs {
   const float* k16t_scale;
 };
 
-// 16 bytes per lane HBM -> LDS: lane l copies base + voff (bytes) to
-// lds_chunk0 + 16*l.  The base is uniform (an SGPR pair, the "saddr" form, so
-// each copy needs one VGPR offset), and so is the LDS destination (M0).
+// LDS byte address of a pointer into a __shared__ array.  Taken where the
+// array itself is named (lds_addr(lk[buf][0])), the cast folds to the
+// array's constant address plus the index arithmetic, all 32-bit and scalar;
+// a generic pointer carried into a helper first costs a 64-bit add and a
+// null check per use.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// 16 bytes per lane HBM -> LDS: lane l copies base + voff (bytes) to LDS
+// byte address lds + 16*l.  The base is uniform (an SGPR pair, the "saddr"
+// form, so each copy needs one VGPR offset), and so is the LDS destination
+// (M0).
 // Issued as inline asm on purpose: the compiler cannot prove that later
 // ds_reads of OTHER ring buffers do not alias the copies in flight, and for
 // the builtin it inserts s_waitcnt vmcnt(0) before every LDS read, which
@@ -76,7 +86,7 @@ struct HotArgs {
 // as clobbered (the compiler notes that it reserves M0): no compiler-generated
 // code in these kernels uses M0 (every M0 write in the kernels' assembly is
 // this statement's), so no value of its own is live across a copy.
-__device__ __forceinline__ void lds_async16(const void* base, unsigned voff, void* lds_chunk0) {
+__device__ __forceinline__ void lds_async16(const void* base, unsigned voff, unsigned lds_chunk0) {
   // readfirstlane is int -> int: both halves go back through unsigned so the
   // low word is zero-extended (a sign-extended low word would corrupt the
   // high word of the address).
@@ -85,8 +95,7 @@ __device__ __forceinline__ void lds_async16(const void* base, unsigned voff, voi
   const unsigned hi =
       static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(b >> 32))));
   const uint64_t sbase = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
-  const unsigned lds = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_chunk0);
+  const unsigned lds = __builtin_amdgcn_readfirstlane(lds_chunk0);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(voff), "s"(sbase), "s"(lds)
@@ -154,7 +163,7 @@ struct TileCopies {
 // invalid tokens, query rows >= T have -inf normalisers, padded columns meet
 // zero register operands).  The host keeps every offset below 2^31 bytes.
 template <int DP, int NW = kWaves>
-__device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_stride, int row0, int T, int dim,
+__device__ __forceinline__ void issue_rows(unsigned tile, const u16* src, int row_stride, int row0, int T, int dim,
                                            int wave, int lane) {
   constexpr int CPR = DP / 8;
   constexpr int NINST = TileCopies<DP>::kRowInst;
@@ -169,7 +178,7 @@ __device__ __forceinline__ void issue_rows(u16* tile, const u16* src, int row_st
     int c = (p % CPR) ^ swz<DP>(r);  // logical chunk stored at this slot (XOR is an involution)
     c = c * 8 < dim ? c : 0;
     const int row = min(row0 + r, T - 1);
-    lds_async16(src, (unsigned)(row * row_stride + c * 8) * 2u, tile + 64 * n * 8);
+    lds_async16(src, (unsigned)(row * row_stride + c * 8) * 2u, tile + 1024u * n);
   }
 }
 
@@ -192,15 +201,15 @@ struct RowCopier {
       voff[i] = (unsigned)(r * row_stride + c * 8) * 2u;
     }
   }
-  __device__ __forceinline__ void issue(u16* tile, const u16* src, int row_stride, int row0, int T, int dim, int wave,
-                                        int lane) const {
+  __device__ __forceinline__ void issue(unsigned tile, const u16* src, int row_stride, int row0, int T, int dim,
+                                        int wave, int lane) const {
     if (row0 + kTile <= T) {
       const u16* base = src + (int64_t)row0 * row_stride;
 #pragma unroll
       for (int i = 0; i < NITER; ++i) {
         const int n = wave + NW * i;
         if (NINST % NW != 0 && n >= NINST) break;
-        lds_async16(base, voff[i], tile + 64 * n * 8);
+        lds_async16(base, voff[i], tile + 1024u * n);
       }
     } else {
       issue_rows<DP, NW>(tile, src, row_stride, row0, T, dim, wave, lane);
@@ -208,8 +217,9 @@ struct RowCopier {
   }
 };
 
-// One copy per wave: 64 bytes (lanes 0-3, 16 each) of `src` into `slot`.
-__device__ __forceinline__ void issue_small(void* slot, const void* src, int lane) {
+// One copy per wave: 64 bytes (lanes 0-3, 16 each) of `src` into LDS byte
+// address `slot`.
+__device__ __forceinline__ void issue_small(unsigned slot, const void* src, int lane) {
   if (lane < 4) lds_async16(src, 16u * lane, slot);
 }
 
@@ -487,9 +497,9 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   auto issue_tile = [&](int it) {
     const int buf = it % kBufs;
     const int j0 = tile_of(it) * kTile;
-    cp_s.issue(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
-    cp_t.issue(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
-    issue_small(ltok[buf][w], tok + j0, lane);
+    cp_s.issue(lds_addr(lk[buf][0]), ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+    cp_t.issue(lds_addr(lk[buf][1]), kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+    issue_small(lds_addr(ltok[buf][w]), tok + j0, lane);
   };
 
   // Software pipeline over 32-key sub-blocks k = 2*tile + sb: the scores of
@@ -845,11 +855,11 @@ __device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
     const int buf = t % kBufs;
     const int j0 = t * kTile;
     if (j == 0)
-      cp_s.issue(lk[buf][0], ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
+      cp_s.issue(lds_addr(lk[buf][0]), ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
     else if (j == 1)
-      cp_t.issue(lk[buf][1], kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
+      cp_t.issue(lds_addr(lk[buf][1]), kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
     else
-      issue_small(ltok[buf][w], tok + j0, lane);
+      issue_small(lds_addr(ltok[buf][w]), tok + j0, lane);
   };
   unsigned g1off[KS];  // this lane's row chunks of a tile: row l32 (+ 32 sb), chunk 2kk + half
 #pragma unroll
@@ -1025,9 +1035,9 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
     auto issue_tile = [&](int it) {
       const int buf = it % kBufs;
       const int i0 = tile_of(it) * kTile;
-      cp_s.issue(lq[buf][0], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
-      cp_t.issue(lq[buf][1], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
-      issue_small(&lnl[buf][16 * w], nl_src + i0, lane);
+      cp_s.issue(lds_addr(lq[buf][0]), qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
+      cp_t.issue(lds_addr(lq[buf][1]), qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
+      issue_small(lds_addr(&lnl[buf][16 * w]), nl_src + i0, lane);
     };
     // the same tile from waves 0-3 only; wave q = w & 3 copies 32 normalisers:
     // student rows 32q.. (q < 2), teacher rows 32(q-2).. (q >= 2)
@@ -1035,9 +1045,9 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
     auto issue_tile4 = [&](int it) {
       const int buf = it % kBufs;
       const int i0 = tile_of(it) * kTile;
-      cq_s.issue(lq[buf][0], qs_base, (int)a.s.q_st, i0, T, a.s.dim, w & 3, lane);
-      cq_t.issue(lq[buf][1], qt_base, (int)a.t.q_st, i0, T, a.t.dim, w & 3, lane);
-      if (lane < 8) lds_async16(nl_src4 + i0, 16u * lane, &lnl[buf][32 * (w & 3)]);
+      cq_s.issue(lds_addr(lq[buf][0]), qs_base, (int)a.s.q_st, i0, T, a.s.dim, w & 3, lane);
+      cq_t.issue(lds_addr(lq[buf][1]), qt_base, (int)a.t.q_st, i0, T, a.t.dim, w & 3, lane);
+      if (lane < 8) lds_async16(nl_src4 + i0, 16u * lane, lds_addr(&lnl[buf][32 * (w & 3)]));
     };
     auto compute_tile = [&](int it) {
       const int buf = it % kBufs;
