@@ -241,7 +241,7 @@ __device__ __forceinline__ void agpr_zero(f32x16* o_s, f32x16* o_t) {
 // register allocator would copy all of them); the fence before the reads is
 // agpr_fence's.
 template <int NDB>
-__device__ __forceinline__ void agpr_rescale(f32x16* o_s, f32x16* o_t, int on, float fs, float ft) {
+__device__ __forceinline__ void agpr_rescale(f32x16* o_s, f32x16* o_t, unsigned on, float fs, float ft) {
   float t0, t1;
   if constexpr (NDB == 4)
     asm volatile("s_cmp_eq_u32 %[on], 0\n\ts_cbranch_scc1 1f\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\t" LARD_RS4(0, 1, 2, 3, fs) LARD_RS4(4, 5, 6, 7, fs) LARD_RS4(8, 9, 10, 11, fs) LARD_RS4(12, 13, 14, 15, fs) LARD_RS4(16, 17, 18, 19, fs) LARD_RS4(20, 21, 22, 23, fs) LARD_RS4(24, 25, 26, 27, fs) LARD_RS4(28, 29, 30, 31, fs) LARD_RS4(32, 33, 34, 35, fs) LARD_RS4(36, 37, 38, 39, fs) LARD_RS4(40, 41, 42, 43, fs) LARD_RS4(44, 45, 46, 47, fs) LARD_RS4(48, 49, 50, 51, fs) LARD_RS4(52, 53, 54, 55, fs) LARD_RS4(56, 57, 58, 59, fs) LARD_RS4(60, 61, 62, 63, fs) LARD_RS4(64, 65, 66, 67, ft) LARD_RS4(68, 69, 70, 71, ft) LARD_RS4(72, 73, 74, 75, ft) LARD_RS4(76, 77, 78, 79, ft) LARD_RS4(80, 81, 82, 83, ft) LARD_RS4(84, 85, 86, 87, ft) LARD_RS4(88, 89, 90, 91, ft) LARD_RS4(92, 93, 94, 95, ft) LARD_RS4(96, 97, 98, 99, ft) LARD_RS4(100, 101, 102, 103, ft) LARD_RS4(104, 105, 106, 107, ft) LARD_RS4(108, 109, 110, 111, ft) LARD_RS4(112, 113, 114, 115, ft) LARD_RS4(116, 117, 118, 119, ft) LARD_RS4(120, 121, 122, 123, ft) LARD_RS4(124, 125, 126, 127, ft) "1:"
@@ -360,7 +360,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   constexpr int EP = 16 / KS;                   // softmax elements per score k-step
   static_assert(PPK * KS == NP, "output products must spread evenly over the score k-steps");
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
-  constexpr int kBufs = 4;
+  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
   // [buffer][student, teacher]; 256-byte aligned for the XOR-form operand
   // addresses (g1b, TrXor)
   __shared__ __attribute__((aligned(256))) u16 lk[kBufs][2][kTile * DP];
@@ -436,7 +436,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   cp_s.init((int)f.k16_st, a.s.dim, w, lane);
   cp_t.init((int)f.k16t_st, a.t.dim, w, lane);
   auto issue_tile = [&](int it) {
-    const int buf = it % kBufs;
+    const int buf = it & (kBufs - 1);
     const int j0 = tile_of(it) * kTile;
     cp_s.issue(lds_addr(lk[buf][0]), ks_base, (int)f.k16_st, j0, T, a.s.dim, w, lane);
     cp_t.issue(lds_addr(lk[buf][1]), kt_base, (int)f.k16t_st, j0, T, a.t.dim, w, lane);
@@ -456,14 +456,19 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     uint64_t tm;  // token validity of its tile, bit j = key j of the tile
   };
   // processing index k -> tile ring buffer and sub-block half
-  auto buf_of = [&](int k) { return (k >> 1) % kBufs; };
+  auto buf_of = [&](int k) { return (k >> 1) & (kBufs - 1); };
+  // Causal: tiles run from the diagonal down, so the tiles that reach this
+  // wave's diagonal sub-block are those of the first kmask steps (pair m of
+  // steps holds tile ntiles-1-m, whose sub-block 2t+1 reaches diag_sb when
+  // t >= diag_sb / 2).  Masking a sub-block of such a tile that lies wholly
+  // below the diagonal, with all tokens valid, changes nothing, so one bound
+  // per wave replaces the per-step sub-block comparison.
+  const int kmask = causal ? 2 * max(ntiles - (diag_sb >> 1), 0) : 0;
   auto prepare = [&](Sub& x, int k) {
-    const int kt0 = tile_of(k >> 1) * kTile;
-    const int sb = k & 1;
-    const int gsb = (kt0 >> 5) + sb;  // global 32-key sub-block index
-    if (x.tm != ~0ull || (causal && gsb >= diag_sb)) {
-      const int first = kt0 + 32 * sb + 4 * half;
-      mask_block_q(x.s, x.t, (unsigned)(x.tm >> (32 * sb + 4 * half)), my_i - first, causal, masked_s, masked_t);
+    if (x.tm != ~0ull || k < kmask) {
+      const int kt0 = tile_of(k >> 1) * kTile;
+      const int first = kt0 + 32 * (k & 1) + 4 * half;
+      mask_block_q(x.s, x.t, (unsigned)(x.tm >> (32 * (k & 1) + 4 * half)), my_i - first, causal, masked_s, masked_t);
     }
   };
 
@@ -604,7 +609,11 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
     }
     score_fence(nxt.s, nxt.t);
     BlockSums bs = {s0 + s1, t0 + t1s, a0 + a1};
-    const bool raise = __any(!(fmaxf(bs.s, bs.t) <= kLazySumQ));  // sums are never NaN; +inf raises
+    // sums are never NaN; +inf raises.  The ballot is wave-uniform: OR-ing its
+    // halves gives the rescale its scalar flag without a VALU round trip.
+    const uint64_t raise_lanes = __ballot(!(fmaxf(bs.s, bs.t) <= kLazySumQ));
+    const bool raise = raise_lanes != 0;
+    const unsigned raise_on = (unsigned)raise_lanes | (unsigned)(raise_lanes >> 32);
     float fs = 1.f, ft = 1.f;
     if (raise) {
       raise_max_row(cur.s, cur.t, R, c2s, c2t, fs, ft);
@@ -615,7 +624,7 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
       pop_s[m] = __builtin_bit_cast(u16x8, (u32x4){ws[4 * m], ws[4 * m + 1], ws[4 * m + 2], ws[4 * m + 3]});
       pop_t[m] = __builtin_bit_cast(u16x8, (u32x4){wt[4 * m], wt[4 * m + 1], wt[4 * m + 2], wt[4 * m + 3]});
     }
-    agpr_rescale<NDB>(o_s, o_t, __builtin_amdgcn_readfirstlane(raise ? 1 : 0), fs, ft);
+    agpr_rescale<NDB>(o_s, o_t, raise_on, fs, ft);
     R.l_s += bs.s;
     R.l_t += bs.t;
     R.acc += bs.a;

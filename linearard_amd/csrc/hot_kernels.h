@@ -441,7 +441,7 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
   // Four tile buffers = two pairs: one pair is consumed while the next lands;
   // one barrier per pair (4 sub-blocks).
-  constexpr int kBufs = 4;
+  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
   __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];  // one copy per wave
 
@@ -495,7 +495,7 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   cp_s.init((int)a.s.k_st, a.s.dim, w, lane);
   cp_t.init((int)a.t.k_st, a.t.dim, w, lane);
   auto issue_tile = [&](int it) {
-    const int buf = it % kBufs;
+    const int buf = it & (kBufs - 1);
     const int j0 = tile_of(it) * kTile;
     cp_s.issue(lds_addr(lk[buf][0]), ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
     cp_t.issue(lds_addr(lk[buf][1]), kt_base, (int)a.t.k_st, j0, T, a.t.dim, w, lane);
@@ -512,7 +512,7 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
     uint64_t tm;  // token validity of its tile, bit j = key j of the tile
   };
   auto scores = [&](Sub& x, int it, int sb) {
-    const int buf = it % kBufs;
+    const int buf = it & (kBufs - 1);
     x.tm = __ballot(ltok[buf][w][lane] != 0);  // read now: the buffer is refilled before its softmax
     sub_scores<DP, BF>(lk[buf][0], 32 * sb, l32, half, fq_s, fq_t, x.s, x.t);
   };
@@ -530,7 +530,7 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   u16x8 pre[2];
   auto step = [&](Sub& cur, int it, int sb, Sub& nxt, int it2, int sb2) {
     prepare(cur, it, sb);
-    const int buf = it2 % kBufs;
+    const int buf = it2 & (kBufs - 1);
     nxt.tm = __ballot(ltok[buf][w][lane] != 0);  // read now: the buffer is refilled before its softmax
     BlockSums bs;
     if (sb2 == 0)
@@ -795,7 +795,7 @@ __device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
   constexpr int KS = DP / 16;
   constexpr int NDB = DP >= 32 ? DP / 32 : 1;  // 32-wide dim blocks of dq
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
-  constexpr int kBufs = 4;
+  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
   __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];
 
@@ -852,7 +852,7 @@ __device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
   cp_s.init((int)a.s.k_st, a.s.dim, w, lane);
   cp_t.init((int)a.t.k_st, a.t.dim, w, lane);
   auto issue_part = [&](int t, int j) {
-    const int buf = t % kBufs;
+    const int buf = t & (kBufs - 1);
     const int j0 = t * kTile;
     if (j == 0)
       cp_s.issue(lds_addr(lk[buf][0]), ks_base, (int)a.s.k_st, j0, T, a.s.dim, w, lane);
@@ -878,9 +878,9 @@ __device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
   // scores of the last sub-block (still in LDS) and drops them.
   auto mphase = [&](int k) {
     const int k1 = min(k, nsub - 1), k2 = max(k - 1, 0);
-    const int buf = (k1 >> 1) % kBufs;
+    const int buf = (k1 >> 1) & (kBufs - 1);
     tm = __ballot(ltok[buf][w][lane] != 0);
-    mfma_phase<DP, BF>(lk[buf][0] + 32 * (k1 & 1) * DP, g1off, fq_s, fq_t, ss, st, lk[(k2 >> 1) % kBufs][0], k2 & 1,
+    mfma_phase<DP, BF>(lk[buf][0] + 32 * (k1 & 1) * DP, g1off, fq_s, fq_t, ss, st, lk[(k2 >> 1) & (kBufs - 1)][0], k2 & 1,
                        tro, dop, dq);
   };
   auto vphase = [&](int k) {
@@ -955,7 +955,7 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
   constexpr int KS = DP / 16;
   constexpr int NDB = DP >= 32 ? DP / 32 : 1;
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
-  constexpr int kBufs = 4;
+  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
   __shared__ __attribute__((aligned(16))) u16 lq[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   // per query row of the tile: -lse*log2(e) of student [0, 64) and teacher [64, 128)
   __shared__ __attribute__((aligned(16))) float lnl[kBufs][2 * kTile];
@@ -1033,7 +1033,7 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
     const float* nl_src = (w < 4 ? f.nl_s : f.nl_t) + bh * f.Tp + 16 * (w & 3);
 
     auto issue_tile = [&](int it) {
-      const int buf = it % kBufs;
+      const int buf = it & (kBufs - 1);
       const int i0 = tile_of(it) * kTile;
       cp_s.issue(lds_addr(lq[buf][0]), qs_base, (int)a.s.q_st, i0, T, a.s.dim, w, lane);
       cp_t.issue(lds_addr(lq[buf][1]), qt_base, (int)a.t.q_st, i0, T, a.t.dim, w, lane);
@@ -1043,14 +1043,14 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
     // student rows 32q.. (q < 2), teacher rows 32(q-2).. (q >= 2)
     const float* nl_src4 = ((w & 3) < 2 ? f.nl_s : f.nl_t) + bh * f.Tp + 32 * (w & 1);
     auto issue_tile4 = [&](int it) {
-      const int buf = it % kBufs;
+      const int buf = it & (kBufs - 1);
       const int i0 = tile_of(it) * kTile;
       cq_s.issue(lds_addr(lq[buf][0]), qs_base, (int)a.s.q_st, i0, T, a.s.dim, w & 3, lane);
       cq_t.issue(lds_addr(lq[buf][1]), qt_base, (int)a.t.q_st, i0, T, a.t.dim, w & 3, lane);
       if (lane < 8) lds_async16(nl_src4 + i0, 16u * lane, lds_addr(&lnl[buf][32 * (w & 3)]));
     };
     auto compute_tile = [&](int it) {
-      const int buf = it % kBufs;
+      const int buf = it & (kBufs - 1);
       const int t = tile_of(it);
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
