@@ -157,7 +157,9 @@ struct TileCopies {
 };
 
 // Issue the async copy of rows [row0, row0 + kTile) x [0, DP) of one head
-// (src = its row 0, rows row_stride elements apart) into a row tile.  Rows
+// (src = its row 0, rows row_stride elements apart) into the row tile at LDS
+// byte address `tile` (lds_addr of the tile; copy n fills bytes
+// [1024 n, 1024 n + 1024) of it).  Rows
 // >= T and column chunks >= dim copy clamped, finite data instead of zeros:
 // every consumer zeroes or masks their contribution (key rows >= T are
 // invalid tokens, query rows >= T have -inf normalisers, padded columns meet
