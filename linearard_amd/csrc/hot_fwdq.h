@@ -360,7 +360,8 @@ __device__ __forceinline__ void hot_fwdq_body(const HotArgs& f, int item) {
   constexpr int EP = 16 / KS;                   // softmax elements per score k-step
   static_assert(PPK * KS == NP, "output products must spread evenly over the score k-steps");
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
-  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
+  constexpr int kBufs = 4;
+  static_assert((kBufs & (kBufs - 1)) == 0, "ring indices are masked with kBufs - 1");
   // [buffer][student, teacher]; 256-byte aligned for the XOR-form operand
   // addresses (g1b, TrXor)
   __shared__ __attribute__((aligned(256))) u16 lk[kBufs][2][kTile * DP];

@@ -443,7 +443,8 @@ __device__ __forceinline__ void hot_fwd_body(const HotArgs& f, int item) {
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;  // K_s rows, K_t rows, token validity
   // Four tile buffers = two pairs: one pair is consumed while the next lands;
   // one barrier per pair (4 sub-blocks).
-  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
+  constexpr int kBufs = 4;
+  static_assert((kBufs & (kBufs - 1)) == 0, "ring indices are masked with kBufs - 1");
   __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];  // one copy per wave
 
@@ -797,7 +798,8 @@ __device__ __forceinline__ void hot_dq_body(const HotArgs& f, int item) {
   constexpr int KS = DP / 16;
   constexpr int NDB = DP >= 32 ? DP / 32 : 1;  // 32-wide dim blocks of dq
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
-  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
+  constexpr int kBufs = 4;
+  static_assert((kBufs & (kBufs - 1)) == 0, "ring indices are masked with kBufs - 1");
   __shared__ __attribute__((aligned(16))) u16 lk[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   __shared__ __attribute__((aligned(16))) unsigned char ltok[kBufs][kWaves][kTile];
 
@@ -957,7 +959,8 @@ __device__ __forceinline__ void hot_bwd_body(const HotArgs& f, int item) {
   constexpr int KS = DP / 16;
   constexpr int NDB = DP >= 32 ? DP / 32 : 1;
   constexpr int kPerWave = 2 * TC::kRowPerWave + 1;
-  constexpr int kBufs = 4;  // a power of two: ring indices are masked, not reduced
+  constexpr int kBufs = 4;
+  static_assert((kBufs & (kBufs - 1)) == 0, "ring indices are masked with kBufs - 1");
   __shared__ __attribute__((aligned(16))) u16 lq[kBufs][2][kTile * DP];  // [buffer][student, teacher]
   // per query row of the tile: -lse*log2(e) of student [0, 64) and teacher [64, 128)
   __shared__ __attribute__((aligned(16))) float lnl[kBufs][2 * kTile];
