@@ -231,8 +231,8 @@ __device__ __forceinline__ void issue_small(unsigned slot, const void* src, int 
 // Softmax state: each lane keeps its own running maxima for its half of the
 // row's keys (lanes l and l+32 share a row), so the loop needs no cross-lane
 // exchange; the halves are merged once at the end.  The maxima are lazy (a
-// rescale only when a sub-block's sums exceed 2^8, see add_block), in raw
-// logit units; a negative scale is handled by flipping
+// rescale only when a sub-block's sums exceed kLazySum = 2^20, see
+// add_block), in raw logit units; a negative scale is handled by flipping
 // the sign of q (exact), so the effective scale is positive.  Masked elements
 // (causal diagonal, invalid keys) are set to -1e30 in place: with running
 // maxima starting at -5e29 their exponentials are exactly 0 and every product

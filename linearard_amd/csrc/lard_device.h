@@ -90,6 +90,13 @@ struct FusedArgs {
   float* row_out;     // [B, Hq, T] per-row KL
 };
 
+// Compile-time flag passed to generic lambdas that are instantiated twice
+// (e.g. per-element work of full and partial tiles).
+template <bool V>
+struct Flag {
+  static constexpr bool value = V;
+};
+
 __device__ __forceinline__ bool mask_at(const void* m, int kind, int64_t idx) {
   if (kind == 1) return static_cast<const unsigned char*>(m)[idx] != 0;
   if (kind == 2) return static_cast<const int32_t*>(m)[idx] != 0;

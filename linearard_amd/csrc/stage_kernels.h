@@ -39,6 +39,7 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
   __shared__ __attribute__((aligned(16))) u16 lkt[HAS_T ? BN * ST : 8];
   __shared__ __attribute__((aligned(16))) u16 lkst[HAS_DQ ? NDB * 32 * TRS : 8];
   __shared__ int lcol[BN];
+  __shared__ int lfull;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
     lse_s = (ls == kNegInf) ? 0.f : ls;
     lse_t = (lt == kNegInf) ? 0.f : lt;
   }
+  const bool wave_ok = __all(ok) != 0;
   float run_m = kNegInf, run_r = 0.f;  // MODE_LSE online max / sum
   float kl_acc = 0.f;                  // MODE_KL
   f32x16 dq[HAS_DQ ? NDB : 1];
@@ -119,9 +121,15 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
     if constexpr (HAS_T) stage_rows<BN, DPT, ST, kStageThreads>(lkt, kt_base, a.t.k_st, j0, T, a.t.dim, tid);
     if constexpr (HAS_DQ)
       stage_rows_transposed<BN, DPS, TRS, kStageThreads>(lkst, ks_base, a.s.k_st, j0, T, a.s.dim, tid);
-    if (tid < BN) {
-      const int j = j0 + tid;
-      lcol[tid] = (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
+    if (tid < 64) {  // wave 0: key validity, and whether the whole tile is valid
+      bool v = true;
+      if (tid < BN) {
+        const int j = j0 + tid;
+        v = (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
+        lcol[tid] = v;
+      }
+      const int all = __all(v);
+      if (tid == 0) lfull = all;
     }
     __syncthreads();
     if (kb > wave_last_kb) continue;
@@ -150,65 +158,80 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
       }
     }
 
-    // Validity of the 16 (i, j) entries this lane holds.
-    bool valid[16];
+    // Per-element work in two forms: full tiles (every key valid, at or
+    // below the diagonal for every row of the wave, every row of the wave
+    // valid) skip the per-element validity; the values of the elements both
+    // forms compute are identical.
+    const bool full = wave_ok && __builtin_amdgcn_readfirstlane(lfull) != 0 && (!a.causal || j0 + BN - 1 <= i0w);
+    auto elements = [&](auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      // Validity of the 16 (i, j) entries this lane holds.
+      bool valid[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int jj = 8 * (r >> 2) + 4 * half + (r & 3);
-      const int j = j0 + jj;
-      valid[r] = ok && lcol[jj] && (!a.causal || j <= my_i);
-    }
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (FULL) {
+          valid[r] = true;
+        } else {
+          const int jj = 8 * (r >> 2) + 4 * half + (r & 3);
+          valid[r] = ok && lcol[jj] && (!a.causal || j0 + jj <= my_i);
+        }
+      }
 
-    if constexpr (MODE == MODE_LSE) {
-      float x[16];
-      float mb = kNegInf;
+      if constexpr (MODE == MODE_LSE) {
+        float x[16];
+        float mb = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        x[r] = valid[r] ? mul_rn(ss[r], a.s.scale) : kNegInf;  // tl.dot(q, k^T) * sm_scale
-        mb = fmaxf(mb, x[r]);
-      }
-      mb = fmaxf(mb, xor32(mb));
-      const float mbs = (mb == kNegInf) ? 0.f : mb;
-      float rs = 0.f;
+        for (int r = 0; r < 16; ++r) {
+          x[r] = valid[r] ? mul_rn(ss[r], a.s.scale) : kNegInf;  // tl.dot(q, k^T) * sm_scale
+          mb = fmaxf(mb, x[r]);
+        }
+        mb = fmaxf(mb, xor32(mb));
+        const float mbs = (mb == kNegInf) ? 0.f : mb;
+        float rs = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) rs += valid[r] ? fast_exp2((x[r] - mbs) * kLog2e) : 0.f;
-      rs += xor32(rs);
-      // Online merge (kernel_A.py:152-154) with the empty-block case guarded.
-      const float mn = fmaxf(run_m, mb);
-      const float f_old = (run_m == kNegInf) ? 0.f : fast_exp2((run_m - mn) * kLog2e);
-      const float f_new = (mb == kNegInf) ? 0.f : fast_exp2((mb - mn) * kLog2e);
-      run_r = run_r * f_old + rs * f_new;
-      run_m = mn;
-    } else if constexpr (MODE == MODE_KL) {
+        for (int r = 0; r < 16; ++r) rs += valid[r] ? fast_exp2((x[r] - mbs) * kLog2e) : 0.f;
+        rs += xor32(rs);
+        // Online merge (kernel_A.py:152-154) with the empty-block case guarded.
+        const float mn = fmaxf(run_m, mb);
+        const float f_old = (run_m == kNegInf) ? 0.f : fast_exp2((run_m - mn) * kLog2e);
+        const float f_new = (mb == kNegInf) ? 0.f : fast_exp2((mb - mn) * kLog2e);
+        run_r = run_r * f_old + rs * f_new;
+        run_m = mn;
+      } else if constexpr (MODE == MODE_KL) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (valid[r]) {
-          const float lps = mul_rn(ss[r], a.s.scale) - lse_s;
-          const float lpt = mul_rn(st[r], a.t.scale) - lse_t;
-          kl_acc += fast_exp2(lpt * kLog2e) * (lpt - lps);
+        for (int r = 0; r < 16; ++r) {
+          if (valid[r]) {
+            const float lps = mul_rn(ss[r], a.s.scale) - lse_s;
+            const float lpt = mul_rn(st[r], a.t.scale) - lse_t;
+            kl_acc += fast_exp2(lpt * kLog2e) * (lpt - lps);
+          }
+        }
+      } else {  // MODE_DQ
+        u16 dv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pd = valid[r] ? fast_exp2((mul_rn(ss[r], a.s.scale) - lse_s) * kLog2e) -
+                                          fast_exp2((mul_rn(st[r], a.t.scale) - lse_t) * kLog2e)
+                                    : 0.f;
+          dv[r] = to_bits(pd, sbf);  // dval.to(qs.dtype)  (kernel_C.py:233)
+        }
+        // dq^T[d][i] += sum_j K^T[d][j] D^T[j][i]
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const u16x8 bop = {dv[8 * m + 0], dv[8 * m + 1], dv[8 * m + 2], dv[8 * m + 3],
+                             dv[8 * m + 4], dv[8 * m + 5], dv[8 * m + 6], dv[8 * m + 7]};
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const u16x8 aop = load_tr_slots(lkst + (32 * db + l32) * TRS, m, half);
+            dq[db] = sbf ? mfma32<true>(aop, bop, dq[db]) : mfma32<false>(aop, bop, dq[db]);
+          }
         }
       }
-    } else {  // MODE_DQ
-      u16 dv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pd = valid[r] ? fast_exp2((mul_rn(ss[r], a.s.scale) - lse_s) * kLog2e) -
-                                        fast_exp2((mul_rn(st[r], a.t.scale) - lse_t) * kLog2e)
-                                  : 0.f;
-        dv[r] = to_bits(pd, sbf);  // dval.to(qs.dtype)  (kernel_C.py:233)
-      }
-      // dq^T[d][i] += sum_j K^T[d][j] D^T[j][i]
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const u16x8 bop = {dv[8 * m + 0], dv[8 * m + 1], dv[8 * m + 2], dv[8 * m + 3],
-                           dv[8 * m + 4], dv[8 * m + 5], dv[8 * m + 6], dv[8 * m + 7]};
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const u16x8 aop = load_tr_slots(lkst + (32 * db + l32) * TRS, m, half);
-          dq[db] = sbf ? mfma32<true>(aop, bop, dq[db]) : mfma32<false>(aop, bop, dq[db]);
-        }
-      }
-    }
+    };
+    if (full)
+      elements(Flag<true>{});
+    else
+      elements(Flag<false>{});
   }
 
   const int64_t row_index = (int64_t)bh * T + my_i;
@@ -256,6 +279,7 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
   __shared__ __attribute__((aligned(16))) float llse_s[BM];
   __shared__ __attribute__((aligned(16))) float llse_t[BM];
   __shared__ int lok[BM];
+  __shared__ int lfull;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -271,6 +295,7 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
   const int my_j = j0w + l32;
   const bool in_range = my_j < T;
   const bool col_valid = in_range && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + my_j);
+  const bool wave_cols_ok = __all(col_valid) != 0;
   const bool sbf = a.s.bf16 != 0;
   const bool tbf = a.t.bf16 != 0;
 
@@ -320,18 +345,24 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
       stage_rows<BM, DPS, SS, kStageThreads>(lqs, qs_base, a.s.q_st, i0, T, a.s.dim, tid);
       stage_rows<BM, DPT, ST, kStageThreads>(lqt, qt_base, a.t.q_st, i0, T, a.t.dim, tid);
       stage_rows_transposed<BM, DPS, TRS, kStageThreads>(lqst, qs_base, a.s.q_st, i0, T, a.s.dim, tid);
-      if (tid < BM) {
-        const int i = i0 + tid;
-        float ls = 0.f, lt = 0.f;
-        bool rv = false;
-        if (i < T) {
-          rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + i);
-          ls = a.lse_s_in[bh * T + i];
-          lt = a.lse_t_in[bh * T + i];
+      if (tid < 64) {  // wave 0: row validity and LSEs, and whether every row is valid
+        bool v = true;
+        if (tid < BM) {
+          const int i = i0 + tid;
+          float ls = 0.f, lt = 0.f;
+          bool rv = false;
+          if (i < T) {
+            rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + i);
+            ls = a.lse_s_in[bh * T + i];
+            lt = a.lse_t_in[bh * T + i];
+          }
+          v = rv && (ls != kNegInf) && (lt != kNegInf);
+          lok[tid] = v;
+          llse_s[tid] = (ls == kNegInf) ? 0.f : ls;
+          llse_t[tid] = (lt == kNegInf) ? 0.f : lt;
         }
-        lok[tid] = rv && (ls != kNegInf) && (lt != kNegInf);
-        llse_s[tid] = (ls == kNegInf) ? 0.f : ls;
-        llse_t[tid] = (lt == kNegInf) ? 0.f : lt;
+        const int all = __all(v);
+        if (tid == 0) lfull = all;
       }
       __syncthreads();
       if (ib < wave_first_ib) continue;
@@ -358,34 +389,46 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
           st = mfma32<false>(*reinterpret_cast<const u16x8*>(lqt + l32 * ST + 16 * kk + 8 * half), fk_t[kk], st);
       }
 
-      u16 dv[16];
+      // Per-element work in two forms: full tiles (every row of the tile and
+      // every column of the wave valid, the whole tile at or below the
+      // diagonal) skip the per-element validity; the values of the elements
+      // both forms compute are identical.
+      const bool full =
+          wave_cols_ok && __builtin_amdgcn_readfirstlane(lfull) != 0 && (!a.causal || j0w + 31 <= i0);
+      auto elements = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        u16 dv[16];
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int ii0 = 8 * r4 + 4 * half;
-        const f32x4 ls4 = *reinterpret_cast<const f32x4*>(llse_s + ii0);
-        const f32x4 lt4 = *reinterpret_cast<const f32x4*>(llse_t + ii0);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int ii0 = 8 * r4 + 4 * half;
+          const f32x4 ls4 = *reinterpret_cast<const f32x4*>(llse_s + ii0);
+          const f32x4 lt4 = *reinterpret_cast<const f32x4*>(llse_t + ii0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * r4 + e;
-          const int i = i0 + ii0 + e;
-          const bool v = lok[ii0 + e] && col_valid && (!a.causal || my_j <= i);
-          const float pd = v ? fast_exp2((mul_rn(ss[r], a.s.scale) - ls4[e]) * kLog2e) -
-                                   fast_exp2((mul_rn(st[r], a.t.scale) - lt4[e]) * kLog2e)
-                             : 0.f;
-          dv[r] = to_bits(pd, sbf);  // kernel_C.py:233
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            const bool v = FULL || (lok[ii0 + e] && col_valid && (!a.causal || my_j <= i0 + ii0 + e));
+            const float pd = v ? fast_exp2((mul_rn(ss[r], a.s.scale) - ls4[e]) * kLog2e) -
+                                     fast_exp2((mul_rn(st[r], a.t.scale) - lt4[e]) * kLog2e)
+                               : 0.f;
+            dv[r] = to_bits(pd, sbf);  // kernel_C.py:233
+          }
         }
-      }
-      // dk^T[d][j] += sum_i Q^T[d][i] D[i][j]
+        // dk^T[d][j] += sum_i Q^T[d][i] D[i][j]
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const u16x8 bop = {dv[8 * m + 0], dv[8 * m + 1], dv[8 * m + 2], dv[8 * m + 3],
-                           dv[8 * m + 4], dv[8 * m + 5], dv[8 * m + 6], dv[8 * m + 7]};
+        for (int m = 0; m < 2; ++m) {
+          const u16x8 bop = {dv[8 * m + 0], dv[8 * m + 1], dv[8 * m + 2], dv[8 * m + 3],
+                             dv[8 * m + 4], dv[8 * m + 5], dv[8 * m + 6], dv[8 * m + 7]};
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const u16x8 aop = load_tr_slots(lqst + (32 * db + l32) * TRS, m, half);
-          dk[db] = sbf ? mfma32<true>(aop, bop, dk[db]) : mfma32<false>(aop, bop, dk[db]);
+          for (int db = 0; db < NDB; ++db) {
+            const u16x8 aop = load_tr_slots(lqst + (32 * db + l32) * TRS, m, half);
+            dk[db] = sbf ? mfma32<true>(aop, bop, dk[db]) : mfma32<false>(aop, bop, dk[db]);
+          }
         }
-      }
+      };
+      if (full)
+        elements(Flag<true>{});
+      else
+        elements(Flag<false>{});
     }
   }
 
