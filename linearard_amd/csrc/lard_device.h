@@ -171,6 +171,58 @@ __device__ __forceinline__ void stage_rows_transposed(u16* lds, const u16* g, in
   }
 }
 
+// The same tile staged through registers in two steps, so that one tile's
+// global loads are in flight while the previous tile is consumed: load()
+// issues the loads (a chunk outside the matrix -- row >= T or column >= dim
+// -- loads row 0, column 0 instead, which exists whenever T > 0, and is
+// remembered as invalid), store() / store_transposed() write the registers to
+// LDS later, zeros for the invalid chunks, exactly what stage_rows /
+// stage_rows_transposed write.
+template <int NROWS, int DP, int NTHREADS>
+struct TileRegs {
+  static constexpr int CPR = DP / 8;  // 16-byte chunks per row
+  static constexpr int NCH = NROWS * CPR;
+  static constexpr int N = (NCH + NTHREADS - 1) / NTHREADS;
+  u16x8 v[N];
+  bool ok[N];
+
+  __device__ __forceinline__ void load(const u16* g, int64_t row_stride, int row0, int T, int dim, int tid) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int c = tid + n * NTHREADS;
+      if (NCH % NTHREADS == 0 || c < NCH) {
+        const int row = row0 + c / CPR;
+        const int dc = (c % CPR) * 8;
+        ok[n] = row < T && dc < dim;
+        v[n] = *reinterpret_cast<const u16x8*>(g + (ok[n] ? (int64_t)row * row_stride + dc : 0));
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(u16* lds, int lds_stride, int tid) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int c = tid + n * NTHREADS;
+      if (NCH % NTHREADS == 0 || c < NCH)
+        *reinterpret_cast<u16x8*>(lds + (c / CPR) * lds_stride + (c % CPR) * 8) = ok[n] ? v[n] : (u16x8)(0);
+    }
+  }
+
+  // lds[d * lds_stride + r]
+  __device__ __forceinline__ void store_transposed(u16* lds, int lds_stride, int tid) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int c = tid + n * NTHREADS;
+      if (NCH % NTHREADS == 0 || c < NCH) {
+        const int r = c / CPR;
+        const int dc = (c % CPR) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lds[(dc + e) * lds_stride + r] = ok[n] ? v[n][e] : (u16)0;
+      }
+    }
+  }
+};
+
 // Load the 8-element k-slot group of a transposed LDS tile for lane `half`
 // and k-step m: slots e=0..3 -> columns 16m+4*half+e, e=4..7 -> 16m+8+4*half+(e-4).
 // This matches the accumulator row order m = 8*(r/4) + 4*half + r%4 of the

@@ -114,13 +114,28 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
   if (a.causal) nkb = min(nkb, (rb * kStageRows + kStageRows - 1) / BN + 1);
   const int wave_last_kb = a.causal ? (i0w + 31) / BN : nkb - 1;
 
+  // Key tiles go through registers: tile kb + 1 is loaded while tile kb is
+  // consumed (except where the registers would not fit: the largest dq
+  // variants load each tile right before storing it).
+  TileRegs<BN, DPS, kStageThreads> rks;
+  TileRegs<BN, HAS_T ? DPT : 16, kStageThreads> rkt;
+  constexpr bool kPrefetch = !(HAS_DQ && DPS == 256 && DPT >= 128);
+  auto load_tile = [&](int j0) {
+    rks.load(ks_base, a.s.k_st, j0, T, a.s.dim, tid);
+    if constexpr (HAS_T) rkt.load(kt_base, a.t.k_st, j0, T, a.t.dim, tid);
+  };
+  if constexpr (kPrefetch) load_tile(0);
+
   for (int kb = 0; kb < nkb; ++kb) {
     const int j0 = kb * BN;
     __syncthreads();
-    stage_rows<BN, DPS, SS, kStageThreads>(lks, ks_base, a.s.k_st, j0, T, a.s.dim, tid);
-    if constexpr (HAS_T) stage_rows<BN, DPT, ST, kStageThreads>(lkt, kt_base, a.t.k_st, j0, T, a.t.dim, tid);
-    if constexpr (HAS_DQ)
-      stage_rows_transposed<BN, DPS, TRS, kStageThreads>(lkst, ks_base, a.s.k_st, j0, T, a.s.dim, tid);
+    if constexpr (!kPrefetch) load_tile(j0);
+    rks.store(lks, SS, tid);
+    if constexpr (HAS_T) rkt.store(lkt, ST, tid);
+    if constexpr (HAS_DQ) rks.store_transposed(lkst, TRS, tid);
+    if constexpr (kPrefetch) {
+      if (kb + 1 < nkb) load_tile(j0 + BN);
+    }
     if (tid < 64) {  // wave 0: key validity, and whether the whole tile is valid
       bool v = true;
       if (tid < BN) {
@@ -339,23 +354,48 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
     const u16* qs_base = a.s.q + (int64_t)b * a.s.q_sb + (int64_t)h * a.s.q_sh;
     const u16* qt_base = a.t.q + (int64_t)b * a.t.q_sb + (int64_t)h * a.t.q_sh;
 
+    // Query tiles and their rows' validity and LSEs go through registers:
+    // tile ib + 1 is loaded while tile ib is consumed (except where the
+    // registers would not fit: the largest variants load each tile right
+    // before storing it).
+    constexpr bool kPrefetch = !(DPS == 256 && DPT >= 128);
+    TileRegs<BM, DPS, kStageThreads> rqs;
+    TileRegs<BM, DPT, kStageThreads> rqt;
+    float nls = 0.f, nlt = 0.f;
+    bool nrv = false;
+    auto load_tile = [&](int i0) {
+      rqs.load(qs_base, a.s.q_st, i0, T, a.s.dim, tid);
+      rqt.load(qt_base, a.t.q_st, i0, T, a.t.dim, tid);
+      if (tid < BM) {
+        const int i = i0 + tid;
+        nrv = false;
+        nls = nlt = 0.f;
+        if (i < T) {
+          nrv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + i);
+          nls = a.lse_s_in[bh * T + i];
+          nlt = a.lse_t_in[bh * T + i];
+        }
+      }
+    };
+    if constexpr (kPrefetch) {
+      if (ib_first < nib) load_tile(ib_first * BM);
+    }
+
     for (int ib = ib_first; ib < nib; ++ib) {
       const int i0 = ib * BM;
       __syncthreads();
-      stage_rows<BM, DPS, SS, kStageThreads>(lqs, qs_base, a.s.q_st, i0, T, a.s.dim, tid);
-      stage_rows<BM, DPT, ST, kStageThreads>(lqt, qt_base, a.t.q_st, i0, T, a.t.dim, tid);
-      stage_rows_transposed<BM, DPS, TRS, kStageThreads>(lqst, qs_base, a.s.q_st, i0, T, a.s.dim, tid);
+      if constexpr (!kPrefetch) load_tile(i0);
+      rqs.store(lqs, SS, tid);
+      rqt.store(lqt, ST, tid);
+      rqs.store_transposed(lqst, TRS, tid);
+      const float ls = nls, lt = nlt;
+      const bool rv = nrv;
+      if constexpr (kPrefetch) {
+        if (ib + 1 < nib) load_tile(i0 + BM);
+      }
       if (tid < 64) {  // wave 0: row validity and LSEs, and whether every row is valid
         bool v = true;
         if (tid < BM) {
-          const int i = i0 + tid;
-          float ls = 0.f, lt = 0.f;
-          bool rv = false;
-          if (i < T) {
-            rv = mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + i);
-            ls = a.lse_s_in[bh * T + i];
-            lt = a.lse_t_in[bh * T + i];
-          }
           v = rv && (ls != kNegInf) && (lt != kNegInf);
           lok[tid] = v;
           llse_s[tid] = (ls == kNegInf) ? 0.f : ls;
