@@ -121,6 +121,20 @@ __device__ __forceinline__ u16 to_bits(float x, bool bf) {
             : __builtin_bit_cast(u16, static_cast<_Float16>(x));
 }
 
+// to_bits for 8 floats at once, in element order: the vector conversion lets
+// the compiler use the two-lane conversions (v_cvt_pk_bf16_f32) and skip the
+// per-element repacking.
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+template <bool BF>
+__device__ __forceinline__ u16x8 to_bits8(const float* x) {
+  const f32x8 v = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  if constexpr (BF) {
+    return __builtin_bit_cast(u16x8, __builtin_convertvector(v, bf16x8));
+  } else {
+    return __builtin_bit_cast(u16x8, __builtin_convertvector(v, f16x8));
+  }
+}
+
 // Rounded product that the compiler may not fuse into a following add:
 // the reference forms scores = dot * sm_scale as a rounded fp32 value before
 // subtracting the LSE (kernel_B.py:190, :206), which makes S - lse exactly 0

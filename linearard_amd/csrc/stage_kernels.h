@@ -222,23 +222,33 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
           }
         }
       } else {  // MODE_DQ
-        u16 dv[16];
+        float pd[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float pd = valid[r] ? fast_exp2((mul_rn(ss[r], a.s.scale) - lse_s) * kLog2e) -
-                                          fast_exp2((mul_rn(st[r], a.t.scale) - lse_t) * kLog2e)
-                                    : 0.f;
-          dv[r] = to_bits(pd, sbf);  // dval.to(qs.dtype)  (kernel_C.py:233)
+          pd[r] = valid[r] ? fast_exp2((mul_rn(ss[r], a.s.scale) - lse_s) * kLog2e) -
+                                 fast_exp2((mul_rn(st[r], a.t.scale) - lse_t) * kLog2e)
+                           : 0.f;
+        }
+        u16x8 dv[2];  // dval.to(qs.dtype)  (kernel_C.py:233)
+        if constexpr (DPS == 256) {
+          // one element at a time: the 8-wide conversions need registers
+          // this variant (128 accumulator registers) does not have
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dv[r >> 3][r & 7] = to_bits(pd[r], sbf);
+        } else if (sbf) {
+          dv[0] = to_bits8<true>(pd);
+          dv[1] = to_bits8<true>(pd + 8);
+        } else {
+          dv[0] = to_bits8<false>(pd);
+          dv[1] = to_bits8<false>(pd + 8);
         }
         // dq^T[d][i] += sum_j K^T[d][j] D^T[j][i]
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-          const u16x8 bop = {dv[8 * m + 0], dv[8 * m + 1], dv[8 * m + 2], dv[8 * m + 3],
-                             dv[8 * m + 4], dv[8 * m + 5], dv[8 * m + 6], dv[8 * m + 7]};
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
             const u16x8 aop = load_tr_slots(lkst + (32 * db + l32) * TRS, m, half);
-            dq[db] = sbf ? mfma32<true>(aop, bop, dq[db]) : mfma32<false>(aop, bop, dq[db]);
+            dq[db] = sbf ? mfma32<true>(aop, dv[m], dq[db]) : mfma32<false>(aop, dv[m], dq[db]);
           }
         }
       }
@@ -437,7 +447,7 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
           wave_cols_ok && __builtin_amdgcn_readfirstlane(lfull) != 0 && (!a.causal || j0w + 31 <= i0);
       auto elements = [&](auto full_tag) {
         constexpr bool FULL = decltype(full_tag)::value;
-        u16 dv[16];
+        float pd[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int ii0 = 8 * r4 + 4 * half;
@@ -447,21 +457,26 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * r4 + e;
             const bool v = FULL || (lok[ii0 + e] && col_valid && (!a.causal || my_j <= i0 + ii0 + e));
-            const float pd = v ? fast_exp2((mul_rn(ss[r], a.s.scale) - ls4[e]) * kLog2e) -
-                                     fast_exp2((mul_rn(st[r], a.t.scale) - lt4[e]) * kLog2e)
-                               : 0.f;
-            dv[r] = to_bits(pd, sbf);  // kernel_C.py:233
+            pd[r] = v ? fast_exp2((mul_rn(ss[r], a.s.scale) - ls4[e]) * kLog2e) -
+                            fast_exp2((mul_rn(st[r], a.t.scale) - lt4[e]) * kLog2e)
+                      : 0.f;
           }
+        }
+        u16x8 dv[2];  // kernel_C.py:233
+        if (sbf) {
+          dv[0] = to_bits8<true>(pd);
+          dv[1] = to_bits8<true>(pd + 8);
+        } else {
+          dv[0] = to_bits8<false>(pd);
+          dv[1] = to_bits8<false>(pd + 8);
         }
         // dk^T[d][j] += sum_i Q^T[d][i] D[i][j]
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-          const u16x8 bop = {dv[8 * m + 0], dv[8 * m + 1], dv[8 * m + 2], dv[8 * m + 3],
-                             dv[8 * m + 4], dv[8 * m + 5], dv[8 * m + 6], dv[8 * m + 7]};
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
             const u16x8 aop = load_tr_slots(lqst + (32 * db + l32) * TRS, m, half);
-            dk[db] = sbf ? mfma32<true>(aop, bop, dk[db]) : mfma32<false>(aop, bop, dk[db]);
+            dk[db] = sbf ? mfma32<true>(aop, dv[m], dk[db]) : mfma32<false>(aop, dv[m], dk[db]);
           }
         }
       };
