@@ -168,30 +168,13 @@ __device__ __forceinline__ void stage_rows(u16* lds, const u16* g, int64_t row_s
   }
 }
 
-// Same source tile, stored transposed: lds[d * LDS_STRIDE + r].
-template <int NROWS, int DP, int LDS_STRIDE, int NTHREADS>
-__device__ __forceinline__ void stage_rows_transposed(u16* lds, const u16* g, int64_t row_stride,
-                                                      int row0, int T, int dim, int tid) {
-  constexpr int CPR = DP / 8;
-#pragma unroll
-  for (int c = tid; c < NROWS * CPR; c += NTHREADS) {
-    const int r = c / CPR;
-    const int dc = (c % CPR) * 8;
-    const int row = row0 + r;
-    u16x8 v = (u16x8)(0);
-    if (row < T && dc < dim) v = *reinterpret_cast<const u16x8*>(g + (int64_t)row * row_stride + dc);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) lds[(dc + e) * LDS_STRIDE + r] = v[e];
-  }
-}
-
 // The same tile staged through registers in two steps, so that one tile's
 // global loads are in flight while the previous tile is consumed: load()
 // issues the loads (a chunk outside the matrix -- row >= T or column >= dim
 // -- loads row 0, column 0 instead, which exists whenever T > 0, and is
 // remembered as invalid), store() / store_transposed() write the registers to
-// LDS later, zeros for the invalid chunks, exactly what stage_rows /
-// stage_rows_transposed write.
+// LDS later, zeros for the invalid chunks (the zero padding stage_rows
+// writes; store_transposed writes lds[d * lds_stride + r]).
 template <int NROWS, int DP, int NTHREADS>
 struct TileRegs {
   static constexpr int CPR = DP / 8;  // 16-byte chunks per row
