@@ -128,6 +128,42 @@ def test_stage_c_kl_backward(gpu_available, dtype, causal, ratio, B, hq, hks, hk
     np.testing.assert_allclose(gk, ek, rtol=rtol, atol=atol)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_stages_on_long_padded_sequences(gpu_available, causal):
+    """Stages A, B, C at T = 700 (ragged against the 32- and 128-row tiles)
+    with GQA on both sides, Ds != Dt, and a mask that leaves most tiles whole
+    (the kernels' full-tile form) and some partial (a padded tail in one
+    sequence; left padding and scattered holes in the other)."""
+    from linearard_amd.attention_KL import kl_backward, kl_forward, lse_stats
+
+    dtype, B, hq, hks, hkt, T, ds, dt = "bf16", 2, 4, 2, 4, 700, 64, 128
+    rng = np.random.default_rng(4100 + int(causal))
+    qs, ks, qt, kt, _ = _two_sided_inputs(rng, dtype, B, hq, hks, hkt, T, ds, dt, None)
+    mask = np.ones((B, T), np.int32)
+    mask[0, T - 150:] = 0
+    mask[1, :40] = 0
+    mask[1, rng.choice(np.arange(40, T), size=T // 10, replace=False)] = 0
+    ss, st = 1 / math.sqrt(ds), 1 / math.sqrt(dt)
+    d = [to_dev(x, dtype) for x in (qs, ks, qt, kt)]
+    m = mask_to_dev(mask)
+    lse_s = lse_stats(d[0], d[1], m, causal, ss)
+    lse_t = lse_stats(d[2], d[3], m, causal, st)
+    np.testing.assert_allclose(lse_s.cpu().numpy(), O.lse_stats(qs, ks, mask, causal, ss), rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(lse_t.cpu().numpy(), O.lse_stats(qt, kt, mask, causal, st), rtol=2e-5, atol=2e-5)
+    out = float(kl_forward(d[0], d[1], lse_s, d[2], d[3], lse_t, m, causal, ss, st).item())
+    ls, lt = lse_s.cpu().numpy(), lse_t.cpu().numpy()
+    ref_b = O.kl_forward(qs, ks, ls, qt, kt, lt, mask, causal, ss, st)
+    assert abs(out - ref_b) <= 1e-4 * max(1.0, abs(ref_b)), (out, ref_b)
+    dq, dk = kl_backward(d[0], d[1], lse_s, d[2], d[3], lse_t, m, causal, ss, st)
+    rq, rk = O.kl_backward(qs, ks, ls, qt, kt, lt, mask, causal, ss, st, d_cast=dtype)
+    for got, ref in ((dq.cpu().numpy(), rq), (dk.cpu().numpy(), rk)):
+        assert np.abs(got - ref).max() <= 5e-3 * max(np.abs(ref).max(), 1e-6)
+    # padded tokens: no gradient in either output
+    dead = mask == 0
+    assert not dq.cpu().numpy()[np.broadcast_to(dead[:, None, :, None], dq.shape)].any()
+    assert not dk.cpu().numpy()[np.broadcast_to(dead[:, None, :, None], dk.shape)].any()
+
+
 @pytest.mark.parametrize("kind", ["bool", "u8", "i32", "i64"])
 def test_mask_dtypes_and_cpu_mask(gpu_available, kind):
     from linearard_amd.attention_KL import lse_stats
