@@ -172,9 +172,8 @@ __device__ __forceinline__ void stage_rows(u16* lds, const u16* g, int64_t row_s
 // global loads are in flight while the previous tile is consumed: load()
 // issues the loads (a chunk outside the matrix -- row >= T or column >= dim
 // -- loads row 0, column 0 instead, which exists whenever T > 0, and is
-// remembered as invalid), store() / store_transposed() write the registers to
-// LDS later, zeros for the invalid chunks (the zero padding stage_rows
-// writes; store_transposed writes lds[d * lds_stride + r]).
+// remembered as invalid), store() writes the registers to LDS later, zeros
+// for the invalid chunks (the zero padding stage_rows writes).
 template <int NROWS, int DP, int NTHREADS>
 struct TileRegs {
   static constexpr int CPR = DP / 8;  // 16-byte chunks per row
@@ -204,30 +203,47 @@ struct TileRegs {
         *reinterpret_cast<u16x8*>(lds + (c / CPR) * lds_stride + (c % CPR) * 8) = ok[n] ? v[n] : (u16x8)(0);
     }
   }
-
-  // lds[d * lds_stride + r]
-  __device__ __forceinline__ void store_transposed(u16* lds, int lds_stride, int tid) const {
-#pragma unroll
-    for (int n = 0; n < N; ++n) {
-      const int c = tid + n * NTHREADS;
-      if (NCH % NTHREADS == 0 || c < NCH) {
-        const int r = c / CPR;
-        const int dc = (c % CPR) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) lds[(dc + e) * lds_stride + r] = ok[n] ? v[n][e] : (u16)0;
-      }
-    }
-  }
 };
 
-// Load the 8-element k-slot group of a transposed LDS tile for lane `half`
-// and k-step m: slots e=0..3 -> columns 16m+4*half+e, e=4..7 -> 16m+8+4*half+(e-4).
-// This matches the accumulator row order m = 8*(r/4) + 4*half + r%4 of the
-// first GEMM, so registers r = 8m..8m+7 of that GEMM are the B operand.
-__device__ __forceinline__ u16x8 load_tr_slots(const u16* row_ptr, int m, int half) {
-  const u16x4 lo = *reinterpret_cast<const u16x4*>(row_ptr + 16 * m + 4 * half);
-  const u16x4 hi = *reinterpret_cast<const u16x4*>(row_ptr + 16 * m + 8 + 4 * half);
-  return (u16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
+// A operand of the second GEMM (m = 32 dims of block db, k-slots = rows
+// 16kk .. 16kk+15 of a row-major [32][STRIDE] LDS tile), read with two
+// transposing LDS loads instead of from a transposed copy.
+// ds_read_b64_tr_b16: in each 16-lane group, lane t receives element t%4 of
+// the 8 bytes that lane 4j + t/4 points at, j = 0..3.  Lane l (group
+// G = l/16, u = l%16) points at row 16kk + 8r + 4(G/2) + u/4, dims
+// 32db + 16(G%2) + 4(u%4) .. +3, so lane l receives, for dim 32db + l%32,
+// rows 16kk + 8r + 4(l/32) + j (k-slots 4r + j): the order (0-3, 8-11,
+// 4-7, 12-15) of the first GEMM's accumulator rows 8(e/4) + 4(l/32) + e%4,
+// whose registers 8kk .. 8kk+7 are the B operand.  DP < 32 (one 16-dim
+// block) repeats dims 0-15 in accumulator rows 16-31, which are never
+// stored.  Addresses: 8-byte aligned (STRIDE a multiple of 4), inside rows
+// 0-31 and dims 0..DP-1.
+template <int DP, int STRIDE>
+struct TrRowTile {
+  static_assert(STRIDE % 4 == 0, "8-byte aligned lane addresses");
+  static constexpr int NDB = DP >= 32 ? DP / 32 : 1;
+  unsigned off[2][NDB];  // u16 elements
+  __device__ __forceinline__ void init(int lane) {
+    const int g = lane >> 4, u = lane & 15;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      int dim = 32 * db + 16 * (g & 1) + 4 * (u & 3);
+      if (DP < 32) dim &= DP - 1;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) off[r][db] = (unsigned)((8 * r + 4 * (g >> 1) + (u >> 2)) * STRIDE + dim);
+    }
+  }
+  __device__ __forceinline__ u16x8 read(const u16* tile, int kk, int db) const {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const u16* base = tile + 16 * kk * STRIDE;
+    s16x4 v[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      v[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)((__attribute__((address_space(3))) u16*)(base + off[r][db])));
+    return __builtin_bit_cast(u16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
 
 }  // namespace lard

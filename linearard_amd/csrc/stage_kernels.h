@@ -13,7 +13,9 @@
 //                               (kernel_C.py:242-253 uses fp32 atomics).
 //
 // DPS/DPT are the head dims padded to a multiple of 16 (D=8 runs as 16 with
-// zero padding, which adds exact zeros to every dot product).
+// zero padding, which adds exact zeros to every dot product).  The second
+// GEMM of stage C (dq, dk) reads its transposed operand straight from the
+// row-major tile of the first with ds_read_b64_tr_b16 (TrRowTile).
 #pragma once
 
 #include "lard_device.h"
@@ -32,12 +34,10 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
   constexpr int KT = DPT / 16;
   constexpr int SS = DPS + 8;  // LDS row strides (elements); +8 breaks bank alignment
   constexpr int ST = DPT + 8;
-  constexpr int TRS = BN + 8;  // transposed tile row stride
   constexpr int NDB = DPS >= 32 ? DPS / 32 : 1;  // 32-wide d blocks of dq
 
   __shared__ __attribute__((aligned(16))) u16 lks[BN * SS];
   __shared__ __attribute__((aligned(16))) u16 lkt[HAS_T ? BN * ST : 8];
-  __shared__ __attribute__((aligned(16))) u16 lkst[HAS_DQ ? NDB * 32 * TRS : 8];
   __shared__ int lcol[BN];
   __shared__ int lfull;
 
@@ -59,11 +59,9 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
   const bool sbf = a.s.bf16 != 0;
   const bool tbf = a.t.bf16 != 0;
 
-  if constexpr (HAS_DQ) {
-    if constexpr (DPS < 32) {  // rows DPS..31 of the transposed tile stay zero
-      for (int c = tid; c < 32 * TRS; c += kStageThreads) lkst[c] = 0;
-    }
-  }
+  // MODE_DQ: K^T operand of the second GEMM, read transposed from lks
+  TrRowTile<DPS, SS> trk;
+  if constexpr (HAS_DQ) trk.init(lane);
 
   // Query fragments (B operand): lane holds q[i = l32][16kk + 8*half .. +7].
   u16x8 fq_s[KS];
@@ -132,7 +130,6 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
     if constexpr (!kPrefetch) load_tile(j0);
     rks.store(lks, SS, tid);
     if constexpr (HAS_T) rkt.store(lkt, ST, tid);
-    if constexpr (HAS_DQ) rks.store_transposed(lkst, TRS, tid);
     if constexpr (kPrefetch) {
       if (kb + 1 < nkb) load_tile(j0 + BN);
     }
@@ -247,7 +244,7 @@ __global__ __launch_bounds__(kStageThreads) void row_kernel(const RelArgs a) {
         for (int m = 0; m < 2; ++m) {
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
-            const u16x8 aop = load_tr_slots(lkst + (32 * db + l32) * TRS, m, half);
+            const u16x8 aop = trk.read(lks, m, db);
             dq[db] = sbf ? mfma32<true>(aop, dv[m], dq[db]) : mfma32<false>(aop, dv[m], dq[db]);
           }
         }
@@ -295,12 +292,10 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
   constexpr int KT = DPT / 16;
   constexpr int SS = DPS + 8;
   constexpr int ST = DPT + 8;
-  constexpr int TRS = BM + 8;
   constexpr int NDB = DPS >= 32 ? DPS / 32 : 1;
 
   __shared__ __attribute__((aligned(16))) u16 lqs[BM * SS];
   __shared__ __attribute__((aligned(16))) u16 lqt[BM * ST];
-  __shared__ __attribute__((aligned(16))) u16 lqst[NDB * 32 * TRS];
   __shared__ __attribute__((aligned(16))) float llse_s[BM];
   __shared__ __attribute__((aligned(16))) float llse_t[BM];
   __shared__ int lok[BM];
@@ -324,9 +319,9 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
   const bool sbf = a.s.bf16 != 0;
   const bool tbf = a.t.bf16 != 0;
 
-  if constexpr (DPS < 32) {
-    for (int c = tid; c < 32 * TRS; c += kStageThreads) lqst[c] = 0;
-  }
+  // Q^T operand of the second GEMM, read transposed from lqs
+  TrRowTile<DPS, SS> trq;
+  trq.init(lane);
 
   // Key fragments (B operand of S[i][j]): lane holds k[j = l32][16kk + 8*half .. +7].
   u16x8 fk_s[KS];
@@ -397,7 +392,6 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
       if constexpr (!kPrefetch) load_tile(i0);
       rqs.store(lqs, SS, tid);
       rqt.store(lqt, ST, tid);
-      rqs.store_transposed(lqst, TRS, tid);
       const float ls = nls, lt = nlt;
       const bool rv = nrv;
       if constexpr (kPrefetch) {
@@ -475,7 +469,7 @@ __global__ __launch_bounds__(kStageThreads) void col_kernel(const RelArgs a) {
         for (int m = 0; m < 2; ++m) {
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
-            const u16x8 aop = load_tr_slots(lqst + (32 * db + l32) * TRS, m, half);
+            const u16x8 aop = trq.read(lqs, m, db);
             dk[db] = sbf ? mfma32<true>(aop, dv[m], dk[db]) : mfma32<false>(aop, dv[m], dk[db]);
           }
         }
