@@ -120,7 +120,7 @@ int lard_kl_backward(const lard_tensor4* qs, const lard_tensor4* ks, const float
 /* Kernels of the autograd calls (lard_attn_kl_forward / _backward), by operands. */
 #define LARD_PATH_THROUGHPUT 0     /* the throughput kernels: one-pass forward (with the row-side gradient), column backward */
 #define LARD_PATH_FUSED_FORWARD 1  /* one-pass forward, stage-kernel backward (several times slower) */
-#define LARD_PATH_STAGE 2          /* stage kernels only: the reference's composition (about 5x slower) */
+#define LARD_PATH_STAGE 2          /* stage kernels only: the reference's composition (about 4x slower) */
 #define LARD_PATH_FLOAT32 3        /* float32 inputs: the double-precision kernels */
 
 /*

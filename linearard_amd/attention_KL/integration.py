@@ -57,7 +57,7 @@ def kernel_path(d, ss: float, st: float):
 
 def _warn_slow_path(d, ss: float, st: float) -> None:
     """One RuntimeWarning per condition that moves a call off the throughput
-    kernels (the stage composition is about 5x slower at d=128)."""
+    kernels (the stage composition is about 4x slower at d=128)."""
     name, why = kernel_path(d, ss, st)
     if name != "throughput" and why not in _WARNED:
         _WARNED.add(why)
