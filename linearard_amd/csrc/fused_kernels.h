@@ -78,11 +78,22 @@ __global__ __launch_bounds__(kStageThreads) void fused_fwd_kernel(const FusedArg
   if (a.causal) nkb = min(nkb, (rb * kStageRows + kStageRows - 1) / BN + 1);
   const int wave_last_kb = a.causal ? (i0w + 31) / BN : nkb - 1;
 
+  // Key tiles go through registers: tile kb + 1 is loaded while tile kb is
+  // consumed.
+  TileRegs<BN, DPS, kStageThreads> rks;
+  TileRegs<BN, DPT, kStageThreads> rkt;
+  rks.load(ks_base, a.s.k_st, 0, T, a.s.dim, tid);
+  rkt.load(kt_base, a.t.k_st, 0, T, a.t.dim, tid);
+
   for (int kb = 0; kb < nkb; ++kb) {
     const int j0 = kb * BN;
     __syncthreads();
-    stage_rows<BN, DPS, SS, kStageThreads>(lks, ks_base, a.s.k_st, j0, T, a.s.dim, tid);
-    stage_rows<BN, DPT, ST, kStageThreads>(lkt, kt_base, a.t.k_st, j0, T, a.t.dim, tid);
+    rks.store(lks, SS, tid);
+    rkt.store(lkt, ST, tid);
+    if (kb + 1 < nkb) {
+      rks.load(ks_base, a.s.k_st, j0 + BN, T, a.s.dim, tid);
+      rkt.load(kt_base, a.t.k_st, j0 + BN, T, a.t.dim, tid);
+    }
     if (tid < BN) {
       const int j = j0 + tid;
       lcol[tid] = (j < T) && mask_at(a.mask, a.mask_kind, (int64_t)b * a.mask_sb + j);
