@@ -150,30 +150,14 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
-// Copy rows [row0, row0+NROWS) x [0, DP) of a [T, D]-strided 16-bit matrix
-// into LDS with row stride LDS_STRIDE (elements).  Rows >= T and columns
-// >= dim are written as zeros, so the MFMA sees exact zero padding.
-template <int NROWS, int DP, int LDS_STRIDE, int NTHREADS>
-__device__ __forceinline__ void stage_rows(u16* lds, const u16* g, int64_t row_stride, int row0,
-                                           int T, int dim, int tid) {
-  constexpr int CPR = DP / 8;  // 16-byte chunks per row
-#pragma unroll
-  for (int c = tid; c < NROWS * CPR; c += NTHREADS) {
-    const int r = c / CPR;
-    const int dc = (c % CPR) * 8;
-    const int row = row0 + r;
-    u16x8 v = (u16x8)(0);
-    if (row < T && dc < dim) v = *reinterpret_cast<const u16x8*>(g + (int64_t)row * row_stride + dc);
-    *reinterpret_cast<u16x8*>(lds + r * LDS_STRIDE + dc) = v;
-  }
-}
-
-// The same tile staged through registers in two steps, so that one tile's
-// global loads are in flight while the previous tile is consumed: load()
-// issues the loads (a chunk outside the matrix -- row >= T or column >= dim
-// -- loads row 0, column 0 instead, which exists whenever T > 0, and is
-// remembered as invalid), store() writes the registers to LDS later, zeros
-// for the invalid chunks (the zero padding stage_rows writes).
+// Rows [row0, row0+NROWS) x [0, DP) of a [T, D]-strided 16-bit matrix,
+// staged into LDS (row stride lds_stride elements) through registers in two
+// steps, so that one tile's global loads are in flight while the previous
+// tile is consumed: load() issues the loads (a chunk outside the matrix --
+// row >= T or column >= dim -- loads row 0, column 0 instead, which exists
+// whenever T > 0, and is remembered as invalid), store() writes the
+// registers to LDS later, zeros for the invalid chunks, so the MFMA sees
+// exact zero padding.
 template <int NROWS, int DP, int NTHREADS>
 struct TileRegs {
   static constexpr int CPR = DP / 8;  // 16-byte chunks per row
