@@ -29,7 +29,7 @@
 // 8 consecutive lanes and reduce with three xor shuffles.  The gradient
 // products read the D tile from LDS; each thread owns D/8 output dims.
 // This path is about exactness, not speed: double FMAs on the VALU (the
-// same rate as float32 on gfx950), one workgroup per CU.
+// same rate as float32 on gfx950), one or two workgroups per CU.
 
 #include "stage_f32.h"
 
@@ -41,13 +41,17 @@ constexpr int kModeFused = 3;            // lse_s, lse_t and the per-row KL in o
 constexpr int kModeRefine = 4;           // lse_s, lse_t in double (for the autograd backward)
 constexpr int kF32Threads = 256;
 constexpr int kF32MaxDim = 256;
-constexpr int kF32Pitch = kF32MaxDim + 4;  // LDS row pitch (floats)
 
+// LDS tiles for head dims up to MAXD (rows padded by 4 floats): the
+// launchers pick the smallest of 64 / 128 / 256 that holds both sides, so
+// d <= 128 fits two workgroups per CU (76 KB each) instead of one (142 KB).
+template <int MAXD>
 struct F32Tiles {
-  float a_s[kF32Rows][kF32Pitch];  // owned rows (student)
-  float a_t[kF32Rows][kF32Pitch];  // owned rows (teacher)
-  float b_s[kF32Rows][kF32Pitch];  // the other side's tile (student)
-  float b_t[kF32Rows][kF32Pitch];  // (teacher)
+  static constexpr int kPitch = MAXD + 4;  // LDS row pitch (floats)
+  float a_s[kF32Rows][kPitch];  // owned rows (student)
+  float a_t[kF32Rows][kPitch];  // owned rows (teacher)
+  float b_s[kF32Rows][kPitch];  // the other side's tile (student)
+  float b_t[kF32Rows][kPitch];  // (teacher)
   double d[kF32Rows][kF32Rows + 1];  // D tile, [owned row][other row]
   double lse_s[kF32Rows], lse_t[kF32Rows];
   unsigned char ok[kF32Rows];        // the other side's row flags (dk)
@@ -55,7 +59,8 @@ struct F32Tiles {
 };
 
 // Rows row0.. of one head into an LDS tile (zeros past T); dim floats each.
-__device__ __forceinline__ void load_rows(float (*dst)[kF32Pitch], const float* base, int64_t row_stride, int row0,
+template <int PITCH>
+__device__ __forceinline__ void load_rows(float (*dst)[PITCH], const float* base, int64_t row_stride, int row0,
                                           int T, int dim) {
   const int q4 = dim / 4;
   for (int idx = threadIdx.x; idx < kF32Rows * q4; idx += kF32Threads) {
@@ -69,7 +74,8 @@ __device__ __forceinline__ void load_rows(float (*dst)[kF32Pitch], const float* 
 
 // S = dot(A[r], B[c + 8 j]) * scale for j = 0..3: exact products of floats
 // summed in double.
-__device__ __forceinline__ void scores(const float (*A)[kF32Pitch], const float (*B)[kF32Pitch], int r, int c, int dim,
+template <int PITCH>
+__device__ __forceinline__ void scores(const float (*A)[PITCH], const float (*B)[PITCH], int r, int c, int dim,
                                        float scale, double (&out)[4]) {
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
   for (int d = 0; d < dim; d += 4) {
@@ -145,9 +151,9 @@ __device__ __forceinline__ const float* kptr(const SideT& s, int b, int g) {
 // ---------------------------------------------------------------------------
 // row modes: LSE (stage A), KL (stage B), DQ (stage C row side)
 // ---------------------------------------------------------------------------
-template <int MODE>
+template <int MODE, int MAXD>
 __global__ __launch_bounds__(kF32Threads) void row_f32_kernel(const RelArgs a) {
-  __shared__ F32Tiles sh;
+  __shared__ F32Tiles<MAXD> sh;
   const int tid = threadIdx.x;
   const int r = tid >> 3, c = tid & 7;
   const int T = a.T;
@@ -182,7 +188,7 @@ __global__ __launch_bounds__(kF32Threads) void row_f32_kernel(const RelArgs a) {
   OnlineLse on_s, on_t;  // LSE and fused modes
   double kl_num = 0.0;   // fused: sum p_t (S_t - S_s) against the teacher's running max
   double kl_acc = 0.0;   // KL mode
-  constexpr int kDq = kF32MaxDim / 32;  // 4-dim groups per thread of dq (dims 4 (c + 8 m) ..)
+  constexpr int kDq = MAXD / 32;  // 4-dim groups per thread of dq (dims 4 (c + 8 m) ..)
   double dq[kDq][4] = {};
 
   for (int j0 = 0; j0 < last; j0 += kF32Rows) {
@@ -305,8 +311,9 @@ __global__ __launch_bounds__(kF32Threads) void row_f32_kernel(const RelArgs a) {
 // ---------------------------------------------------------------------------
 // column side: dk (stage C), one owner per key row and student kv head
 // ---------------------------------------------------------------------------
+template <int MAXD>
 __global__ __launch_bounds__(kF32Threads) void col_f32_kernel(const RelArgs a) {
-  __shared__ F32Tiles sh;
+  __shared__ F32Tiles<MAXD> sh;
   const int tid = threadIdx.x;
   const int r = tid >> 3, c = tid & 7;
   const int T = a.T;
@@ -319,7 +326,7 @@ __global__ __launch_bounds__(kF32Threads) void col_f32_kernel(const RelArgs a) {
 
   const bool lse_f32 = a.lse64_in == nullptr;
   load_rows(sh.a_s, kptr(a.s, b, g), a.s.k_st, j0, T, a.s.dim);
-  constexpr int kDk = kF32MaxDim / 32;
+  constexpr int kDk = MAXD / 32;
   double dk[kDk][4] = {};
 
   int loaded_t = -1;  // teacher kv head whose key rows are in a_t
@@ -392,40 +399,47 @@ __global__ __launch_bounds__(kF32Threads) void col_f32_kernel(const RelArgs a) {
 
 dim3 row_grid(const RelArgs& a) { return dim3((a.T + kF32Rows - 1) / kF32Rows, a.B * a.Hq); }
 
+// The smallest tile width of 64 / 128 / 256 that holds both sides' dims.
+int tile_dims(const RelArgs& a) {
+  const int d = a.s.dim > a.t.dim ? a.s.dim : a.t.dim;
+  return d <= 64 ? 64 : d <= 128 ? 128 : kF32MaxDim;
+}
+
+template <int MODE>
+hipError_t launch_row(const RelArgs& a, hipStream_t stream) {
+  switch (tile_dims(a)) {
+    case 64: hipLaunchKernelGGL((row_f32_kernel<MODE, 64>), row_grid(a), dim3(kF32Threads), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((row_f32_kernel<MODE, 128>), row_grid(a), dim3(kF32Threads), 0, stream, a); break;
+    default: hipLaunchKernelGGL((row_f32_kernel<MODE, kF32MaxDim>), row_grid(a), dim3(kF32Threads), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
-hipError_t launch_row_lse_f32(const RelArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((row_f32_kernel<MODE_LSE>), row_grid(a), dim3(kF32Threads), 0, stream, a);
-  return hipGetLastError();
-}
+hipError_t launch_row_lse_f32(const RelArgs& a, hipStream_t stream) { return launch_row<MODE_LSE>(a, stream); }
 
-hipError_t launch_row_kl_f32(const RelArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((row_f32_kernel<MODE_KL>), row_grid(a), dim3(kF32Threads), 0, stream, a);
-  return hipGetLastError();
-}
+hipError_t launch_row_kl_f32(const RelArgs& a, hipStream_t stream) { return launch_row<MODE_KL>(a, stream); }
 
 hipError_t launch_fused_fwd_f32(const FusedArgs& f, hipStream_t stream) {
   RelArgs a = f.r;  // the fused mode writes lse_s to lse_out, lse_t to dq_out (as floats), the KL to row_out
   a.lse_out = f.lse_s_out;
   a.dq_out = f.lse_t_out;
   a.row_out = f.row_out;
-  hipLaunchKernelGGL((row_f32_kernel<kModeFused>), row_grid(a), dim3(kF32Threads), 0, stream, a);
-  return hipGetLastError();
+  return launch_row<kModeFused>(a, stream);
 }
 
-hipError_t launch_refine_lse_f32(const RelArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((row_f32_kernel<kModeRefine>), row_grid(a), dim3(kF32Threads), 0, stream, a);
-  return hipGetLastError();
-}
+hipError_t launch_refine_lse_f32(const RelArgs& a, hipStream_t stream) { return launch_row<kModeRefine>(a, stream); }
 
-hipError_t launch_row_dq_f32(const RelArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((row_f32_kernel<MODE_DQ>), row_grid(a), dim3(kF32Threads), 0, stream, a);
-  return hipGetLastError();
-}
+hipError_t launch_row_dq_f32(const RelArgs& a, hipStream_t stream) { return launch_row<MODE_DQ>(a, stream); }
 
 hipError_t launch_col_dk_f32(const RelArgs& a, hipStream_t stream) {
   const dim3 grid((a.T + kF32Rows - 1) / kF32Rows, a.B * a.s.hkv);
-  hipLaunchKernelGGL(col_f32_kernel, grid, dim3(kF32Threads), 0, stream, a);
+  switch (tile_dims(a)) {
+    case 64: hipLaunchKernelGGL(col_f32_kernel<64>, grid, dim3(kF32Threads), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL(col_f32_kernel<128>, grid, dim3(kF32Threads), 0, stream, a); break;
+    default: hipLaunchKernelGGL(col_f32_kernel<kF32MaxDim>, grid, dim3(kF32Threads), 0, stream, a);
+  }
   return hipGetLastError();
 }
 
